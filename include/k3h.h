@@ -1,0 +1,110 @@
+/* k3h: C-ABI for the MI355X (gfx950) K3 prefill memory-bound op family.
+ *
+ * Two layers:
+ *
+ * 1. Module layer -- the drop-in for the kern runtime's cubin loading.  The
+ *    reference runtime loads one code object per module key (kernels.toml:66-76,
+ *    126-135, 203-230, 243-253) and launches `extern "C"` entries with a packed
+ *    parameter buffer laid out at natural alignment (pointers / i64 at 8 bytes,
+ *    i32 / f32 at 4), grid and block from the manifest's launch description
+ *    (manifest ops.<op>.impl.launches, e.g. k3-tp4-prefill-16k.json:404788).
+ *    k3h_module_* / k3h_function / k3h_launch do the same over hipModule with
+ *    gfx950 code objects that export the same entry names.
+ *
+ * 2. Operator layer -- one typed wrapper per hot manifest op, computing grid and
+ *    block exactly as the manifest's grid expressions do, validating arguments
+ *    on the host, and launching on the caller's stream.
+ *
+ * Conventions: every function returns K3H_OK (0) or a negative code; a HIP
+ * error e is returned as K3H_EHIP_BASE - e.  No exceptions cross the ABI.
+ * Streams are hipStream_t passed as void* (NULL = the default stream).  Device
+ * pointers are plain pointers; bf16 tensors are 16-bit patterns, e4m3 / E8M0
+ * tensors bytes.  Launches are stream-ordered, allocate nothing and are
+ * graph-capturable.  Module handles are immutable after load; a context
+ * serialises its lazy module loads internally and may be shared by threads.
+ */
+#ifndef K3H_H
+#define K3H_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define K3H_API __attribute__((visibility("default")))
+
+#define K3H_OK 0
+#define K3H_EINVAL (-1)    /* bad argument: null/misaligned pointer, size, range */
+#define K3H_ENOMODULE (-2) /* code object missing or not loadable */
+#define K3H_ENOENTRY (-3)  /* entry name not in the module */
+#define K3H_ENOMEM (-4)
+#define K3H_EHIP_BASE (-1000)
+
+typedef struct k3h_module_s* k3h_module_t;
+typedef struct k3h_fn_s* k3h_fn_t;
+typedef struct k3h_ctx_s* k3h_ctx_t;
+
+/* ---- module layer --------------------------------------------------------
+ * Replaces the kern runtime's cubin load / entry lookup / launch (README.md:92-97
+ * of the reference; manifest `modules` and `impl.launches`). */
+K3H_API int k3h_module_load(const void* image, size_t bytes, k3h_module_t* out);
+K3H_API int k3h_module_load_file(const char* path, k3h_module_t* out);
+K3H_API int k3h_function(k3h_module_t mod, const char* entry, k3h_fn_t* out);
+K3H_API int k3h_launch(k3h_fn_t fn, const uint32_t grid[3], const uint32_t block[3],
+                       uint32_t shmem, void* stream, const void* packed_args, size_t bytes);
+K3H_API int k3h_module_unload(k3h_module_t mod);
+K3H_API const char* k3h_error_string(int code);
+/* HIP runtime version the library is bound to (hipRuntimeGetVersion). */
+K3H_API int k3h_runtime_version(int* version);
+
+/* ---- context: code objects by module key ---------------------------------
+ * <dir>/<module key>.hsaco, loaded on first use (e.g. "k3_residual_v2+LAND_BF16=1"). */
+K3H_API int k3h_ctx_create(const char* codeobj_dir, k3h_ctx_t* out);
+K3H_API int k3h_ctx_destroy(k3h_ctx_t ctx);
+K3H_API int k3h_ctx_function(k3h_ctx_t ctx, const char* module_key, const char* entry,
+                             k3h_fn_t* out);
+
+/* ---- K1 residual family ---------------------------------------------------
+ * eps selects the code object: 1e-5 (the reference's compiled KEPS,
+ * k3_residual_v2.cu:54) or 1e-6 (the "+K3_EPS=1e-6f" build); others: K3H_EINVAL. */
+
+/* kern_k3_land_add_attnres_rms (k3_residual_v2.cu:295; manifest op
+ * land_add_attnres_rms_bf16_v2, l0-bf16 json:401328).  grid (B), block 128.
+ * land_bf16 != 0: partial is bf16 [B,7168] (module +LAND_BF16=1), else f32. */
+K3H_API int k3h_land_add_attnres_rms(k3h_ctx_t ctx, void* stream, int land_bf16,
+                                     const void* partial, const void* prefix,
+                                     const void* blocks, const float* sw, const void* gamma,
+                                     void* prefix2, void* normed, int nb, int snapshot, int B,
+                                     float eps);
+/* kern_k3_land_add_attnres_rms_nb{1..8} (k3_residual_nb.cu:350-811; manifest op
+ * land_add_attnres_rms_bf16_v2_nb1, json:406888).  LAND_BF16 only; 1 <= nb <= 8. */
+K3H_API int k3h_land_add_attnres_rms_nb(k3h_ctx_t ctx, void* stream, const void* partial,
+                                        const void* prefix, const void* blocks, const float* sw,
+                                        const void* gamma, void* prefix2, void* normed, int nb,
+                                        int snapshot, int B);
+/* kern_k3_attnres_rms (k3_residual_v2.cu:260; op attnres_rms_v2, l0-bf16 json:401191). */
+K3H_API int k3h_attnres_rms(k3h_ctx_t ctx, void* stream, const void* prefix, void* blocks,
+                            const float* sw, const void* gamma, void* normed, int nb,
+                            int snapshot, int B, float eps);
+/* kern_k3_land_add2 (k3_residual_v2.cu:349; op land_add2_v2, l0-bf16 json:401295). */
+K3H_API int k3h_land_add2(k3h_ctx_t ctx, void* stream, const float* p1, const float* p2,
+                          const void* prefix2, void* hidden, int two, int B);
+
+/* ---- MXFP8 -----------------------------------------------------------------
+ * kern_k3_moe_quant (k3_moe_prefill_v4.cu:111; manifest op moe_quant, json:404926).
+ * grid ceil(rows*cols/32/256), block 256; rows*cols % 32 == 0. */
+K3H_API int k3h_moe_quant(k3h_ctx_t ctx, void* stream, const void* x, void* q, void* sf,
+                          int rows, int cols);
+
+/* k3h_residual_rms_mxfp8: fused residual add + RMSNorm + MXFP8 (no single
+ * reference entry: K1b at nb = 0 composed with kern_k3_moe_quant).  Module
+ * k3h_fused; grid (B), block 128.  normed may be NULL. */
+K3H_API int k3h_residual_rms_mxfp8(k3h_ctx_t ctx, void* stream, const void* x,
+                                   const void* residual, const void* gamma, void* residual_out,
+                                   void* q, void* sf, void* normed, float eps, int B);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,31 @@
+// Module k3_residual_nb+LAND_BF16=1: K1b with the candidate count fixed per entry.
+//
+//   kern_k3_land_add_attnres_rms_nb{1..8}(partial, prefix, blocks, sw, gamma,
+//                                         prefix2, normed, nb_in, snapshot, B)
+//
+// Same parameters, geometry (grid (B,1,1), block 128) and arithmetic as
+// kern_k3_land_add_attnres_rms; the entry for k returns at once unless
+// nb_in == k (reference: k3_residual_nb.cu:350-811).  Fixing nb lets the
+// compiler drop the unused candidate registers.
+#include "k3_residual_row.h"
+
+#define K3_NB_ENTRY(K)                                                                      \
+  extern "C" __global__ void __launch_bounds__(K3_RES_THREADS)                              \
+      kern_k3_land_add_attnres_rms_nb##K(                                                   \
+          const k3_land_t* __restrict__ partial, const uint16_t* __restrict__ prefix,       \
+          const uint16_t* __restrict__ blocks, const float* __restrict__ sw,                \
+          const uint16_t* __restrict__ gamma, uint16_t* __restrict__ prefix2,               \
+          uint16_t* __restrict__ normed, int nb_in, int snapshot, int B) {                  \
+    if (nb_in != K) return;                                                                 \
+    k3_land_add_attnres_rms_body<K>(partial, prefix, blocks, sw, gamma, prefix2, normed, K, \
+                                    snapshot, B);                                           \
+  }
+
+K3_NB_ENTRY(1)
+K3_NB_ENTRY(2)
+K3_NB_ENTRY(3)
+K3_NB_ENTRY(4)
+K3_NB_ENTRY(5)
+K3_NB_ENTRY(6)
+K3_NB_ENTRY(7)
+K3_NB_ENTRY(8)

@@ -1,0 +1,262 @@
+// K1 residual-stream row body for gfx950: AttnRes candidate mixing + RMSNorm of
+// one 7168-wide bf16 row, computed by one 128-thread workgroup (two wave64s).
+//
+// Semantics follow the reference row body (k3_residual_v2.cu:107-257):
+//   * candidates c < nb are rows blocks[b, c, :]; candidate nb is the prefix
+//     row held in registers (pv);
+//   * sq_c = sum x^2, dp_c = sum x * sw; score_c = dp_c * rsqrt(sq_c / H + eps);
+//     p = softmax(score); mixed = bf16(sum_c p_c * x_c) in f32;
+//   * r = rsqrt(sum mixed^2 / H + eps); normed = bf16(bf16(mixed * r) (x) gamma)
+//     where (x) is the bf16 x bf16 -> bf16 product.
+//
+// Ownership and reduction order: thread t owns the 16-byte vectors
+// u = t + 128 v (v < 7) of the row, i.e. elements 8u .. 8u + 7, so each wave
+// issues 1 KB of contiguous loads per vector step.  Per-thread sums run over v
+// (outer) and the eight elements (inner) with one fma each; a 32-lane xor
+// butterfly follows inside each half-wave, and the four half-wave partials are
+// added in half-wave order.  That is the order of the reference's 128-thread
+// row (k3_residual_v2.cu:229-242), so the CPU checker can replay it exactly.
+// rsqrt is 1 / sqrt with both operations correctly rounded; the softmax uses
+// the deterministic k3_expf.  Both therefore have an exact CPU counterpart.
+#pragma once
+#include "../common/k3_dev.h"
+
+#define K3_H 7168
+#define K3_NB_MAX 8
+#define K3_RES_THREADS 128
+#define K3_KVPT 7                 /* 16-byte vectors per thread: 896 / 128 */
+#define K3_NHW (K3_RES_THREADS / 32)  /* half-waves per workgroup */
+
+#ifndef K3_EPS
+#define K3_EPS 1e-5f
+#endif
+
+K3_DEV int k3_vec_off(int t, int v) { return (t + v * K3_RES_THREADS) * 8; }
+
+// Sum of squares of this thread's vectors, reference order.
+K3_DEV float k3_row_sumsq(const k3_u4* pv) {
+  float sq = 0.0f;
+#pragma unroll
+  for (int v = 0; v < K3_KVPT; ++v) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float lo = k3_bf_lo(pv[v][j]), hi = k3_bf_hi(pv[v][j]);
+      sq = __builtin_fmaf(lo, lo, sq);
+      sq = __builtin_fmaf(hi, hi, sq);
+    }
+  }
+  return sq;
+}
+
+// Block-wide total of a per-thread partial: half-wave butterfly, then the four
+// half-wave partials added in order.  `red` is K3_NHW floats of LDS.  Ends with
+// a barrier so `red` may be reused.
+K3_DEV float k3_block_sum128(float part, float* red, int t) {
+  part = k3_sum32(part);
+  if ((t & 31) == 0) red[t >> 5] = part;
+  __syncthreads();
+  float tot = 0.0f;
+#pragma unroll
+  for (int w = 0; w < K3_NHW; ++w) tot += red[w];
+  __syncthreads();
+  return tot;
+}
+
+// 1 / sqrt(sum / H + eps); the reference writes rsqrtf(sum * (1/H) + eps),
+// which its compiler contracts into one fma.
+K3_DEV float k3_row_rscale(float tot, float eps) {
+  return k3_rsqrt_cr(__builtin_fmaf(tot, 1.0f / (float)K3_H, eps));
+}
+
+// AttnRes mixing: replaces pv (the prefix candidate) by the mixed row.
+// NBC >= 0 fixes nb at compile time; NBC < 0 takes the run-time nb.
+template <int NBC>
+K3_DEV void k3_attnres_mix(const uint16_t* __restrict__ blk_row, k3_u4* pv,
+                           const float* __restrict__ sw, int nb_rt, float eps, int t) {
+  const int nb = NBC >= 0 ? NBC : nb_rt;
+  if (nb <= 0) return;  // mixed = prefix: bf16(1.0f * f32(prefix)) == prefix
+  __shared__ float s_red[(K3_NB_MAX + 1) * 2 * K3_NHW];
+  const int lane32 = t & 31, hw = t >> 5;
+
+  // pass 1: sum x^2 and sum x * sw per candidate (prefix kept at index K3_NB_MAX)
+  float sq[K3_NB_MAX + 1], dp[K3_NB_MAX + 1];
+#pragma unroll
+  for (int c = 0; c <= K3_NB_MAX; ++c) { sq[c] = 0.0f; dp[c] = 0.0f; }
+#pragma unroll
+  for (int v = 0; v < K3_KVPT; ++v) {
+    const int u = k3_vec_off(t, v);
+    const float4 a = *(const float4*)(sw + u);
+    const float4 b = *(const float4*)(sw + u + 4);
+    const float swv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float lo = k3_bf_lo(pv[v][j]), hi = k3_bf_hi(pv[v][j]);
+      sq[K3_NB_MAX] = __builtin_fmaf(lo, lo, sq[K3_NB_MAX]);
+      sq[K3_NB_MAX] = __builtin_fmaf(hi, hi, sq[K3_NB_MAX]);
+      dp[K3_NB_MAX] = __builtin_fmaf(lo, swv[2 * j], dp[K3_NB_MAX]);
+      dp[K3_NB_MAX] = __builtin_fmaf(hi, swv[2 * j + 1], dp[K3_NB_MAX]);
+    }
+#pragma unroll
+    for (int c = 0; c < K3_NB_MAX; ++c) {
+      if (c >= nb) break;
+      const k3_u4 x = k3_ld16(blk_row + (size_t)c * K3_H + u);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float lo = k3_bf_lo(x[j]), hi = k3_bf_hi(x[j]);
+        sq[c] = __builtin_fmaf(lo, lo, sq[c]);
+        sq[c] = __builtin_fmaf(hi, hi, sq[c]);
+        dp[c] = __builtin_fmaf(lo, swv[2 * j], dp[c]);
+        dp[c] = __builtin_fmaf(hi, swv[2 * j + 1], dp[c]);
+      }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < K3_NB_MAX; ++c) {
+    if (c >= nb) break;
+    const float s = k3_sum32(sq[c]);
+    const float d = k3_sum32(dp[c]);
+    if (lane32 == 0) { s_red[(2 * c) * K3_NHW + hw] = s; s_red[(2 * c + 1) * K3_NHW + hw] = d; }
+  }
+  {
+    const float s = k3_sum32(sq[K3_NB_MAX]);
+    const float d = k3_sum32(dp[K3_NB_MAX]);
+    if (lane32 == 0) { s_red[(2 * nb) * K3_NHW + hw] = s; s_red[(2 * nb + 1) * K3_NHW + hw] = d; }
+  }
+  __syncthreads();
+
+  // scores and softmax: lane c of every half-wave handles candidate c
+  const int ncand = nb + 1;
+  float sc = -3.0e38f;
+  if (lane32 < ncand) {
+    float sqv = 0.0f, dpv = 0.0f;
+#pragma unroll
+    for (int w = 0; w < K3_NHW; ++w) {
+      sqv += s_red[(2 * lane32) * K3_NHW + w];
+      dpv += s_red[(2 * lane32 + 1) * K3_NHW + w];
+    }
+    sc = dpv * k3_row_rscale(sqv, eps);
+  }
+  const float mx = k3_max32(sc);
+  float ex = 0.0f;
+  if (lane32 < ncand) {
+    const float d = sc - mx;
+    ex = d < -87.0f ? 0.0f : k3_expf(d);
+  }
+  const float den = k3_sum32(ex);
+  const float pmine = ex / den;
+  const int base = t & 32;  // lanes of this half-wave within the wave
+  float p[K3_NB_MAX];
+#pragma unroll
+  for (int c = 0; c < K3_NB_MAX; ++c) p[c] = __shfl(pmine, base + c, 64);
+  const float pp = __shfl(pmine, base + nb, 64);
+
+  // pass 2: f32 mix, one bf16 landing per value
+#pragma unroll
+  for (int v = 0; v < K3_KVPT; ++v) {
+    const int u = k3_vec_off(t, v);
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc[2 * j] = pp * k3_bf_lo(pv[v][j]);
+      acc[2 * j + 1] = pp * k3_bf_hi(pv[v][j]);
+    }
+#pragma unroll
+    for (int c = 0; c < K3_NB_MAX; ++c) {
+      if (c >= nb) break;
+      const k3_u4 x = k3_ld16(blk_row + (size_t)c * K3_H + u);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[2 * j] = __builtin_fmaf(p[c], k3_bf_lo(x[j]), acc[2 * j]);
+        acc[2 * j + 1] = __builtin_fmaf(p[c], k3_bf_hi(x[j]), acc[2 * j + 1]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pv[v][j] = k3_pack_bf2(acc[2 * j], acc[2 * j + 1]);
+  }
+}
+
+// normed = bf16(bf16(mixed * r) (x) gamma) for this thread's vectors; returns
+// the normed vectors in `nv`.
+K3_DEV void k3_rms_apply(const k3_u4* pv, const uint16_t* __restrict__ gamma, float r,
+                         k3_u4* nv, int t) {
+#pragma unroll
+  for (int v = 0; v < K3_KVPT; ++v) {
+    const k3_u4 g = k3_ld16(gamma + k3_vec_off(t, v));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t y = k3_pack_bf2(k3_bf_lo(pv[v][j]) * r, k3_bf_hi(pv[v][j]) * r);
+      nv[v][j] = k3_mul_bf2(y, g[j]);
+    }
+  }
+}
+
+// The whole row body: mixing (if any), RMS, normed store.
+template <int NBC>
+K3_DEV void k3_attnres_rms_row(const uint16_t* __restrict__ blk_row, k3_u4* pv,
+                               const float* __restrict__ sw, const uint16_t* __restrict__ gamma,
+                               uint16_t* __restrict__ normed_row, int nb, float eps, int t) {
+  __shared__ float s_red2[K3_NHW];
+  k3_attnres_mix<NBC>(blk_row, pv, sw, nb, eps, t);
+  const float tot = k3_block_sum128(k3_row_sumsq(pv), s_red2, t);
+  const float r = k3_row_rscale(tot, eps);
+  k3_u4 nv[K3_KVPT];
+  k3_rms_apply(pv, gamma, r, nv, t);
+#pragma unroll
+  for (int v = 0; v < K3_KVPT; ++v) k3_st16(normed_row + k3_vec_off(t, v), nv[v]);
+}
+
+// K1b landing: prefix2 = snapshot ? bf16(pf) : bf16(f32(prefix) + f32(bf16(pf))).
+// LAND_BF16 = partial arrives as bf16 (bf16(pf) == pf); otherwise f32.
+#ifdef LAND_BF16
+typedef uint16_t k3_land_t;
+#else
+typedef float k3_land_t;
+#endif
+
+K3_DEV k3_u4 k3_load_land(const k3_land_t* __restrict__ partial, size_t off) {
+#ifdef LAND_BF16
+  return k3_ld16(partial + off);
+#else
+  const float4 a = *(const float4*)(partial + off);
+  const float4 c = *(const float4*)(partial + off + 4);
+  k3_u4 w;
+  w[0] = k3_pack_bf2(a.x, a.y);
+  w[1] = k3_pack_bf2(a.z, a.w);
+  w[2] = k3_pack_bf2(c.x, c.y);
+  w[3] = k3_pack_bf2(c.z, c.w);
+  return w;
+#endif
+}
+
+K3_DEV k3_u4 k3_add_land(k3_u4 prefix, k3_u4 landed) {
+  k3_u4 o;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    o[j] = k3_pack_bf2(k3_bf_lo(prefix[j]) + k3_bf_lo(landed[j]),
+                       k3_bf_hi(prefix[j]) + k3_bf_hi(landed[j]));
+  return o;
+}
+
+// K1b entry body shared by the run-time-nb entry and the per-nb entries.
+template <int NBC>
+K3_DEV void k3_land_add_attnres_rms_body(const k3_land_t* __restrict__ partial,
+                                         const uint16_t* __restrict__ prefix,
+                                         const uint16_t* __restrict__ blocks,
+                                         const float* __restrict__ sw,
+                                         const uint16_t* __restrict__ gamma,
+                                         uint16_t* __restrict__ prefix2,
+                                         uint16_t* __restrict__ normed, int nb, int snapshot, int B) {
+  const int b = blockIdx.x;
+  if (b >= B) return;
+  const int t = threadIdx.x;
+  k3_u4 pv[K3_KVPT];
+#pragma unroll
+  for (int v = 0; v < K3_KVPT; ++v) {
+    const size_t off = (size_t)b * K3_H + k3_vec_off(t, v);
+    const k3_u4 l = k3_load_land(partial, off);
+    pv[v] = snapshot ? l : k3_add_land(k3_ld16(prefix + off), l);
+    k3_st16(prefix2 + off, pv[v]);
+  }
+  k3_attnres_rms_row<NBC>(blocks + (size_t)b * K3_NB_MAX * K3_H, pv, sw, gamma,
+                          normed + (size_t)b * K3_H, nb, K3_EPS, t);
+}

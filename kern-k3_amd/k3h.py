@@ -1,0 +1,313 @@
+"""Python host side of the k3h C-ABI (``include/k3h.h``).
+
+The operators mirror the reference's manifest op surface: each method has the
+manifest op's parameters in the manifest's order (``ops.<op>.params`` of
+k3-tp4-prefill-16k.json, e.g. ``moe_quant`` at line 404926) and launches the
+gfx950 code object with the manifest's grid.  Tensors are torch device tensors
+(torch provides the memory and the stream; the arithmetic is the HIP kernels').
+Arguments are checked here and again in the C library; a failed check raises
+``ValueError``, a failed launch ``K3HError``.  There is no CPU path: a missing
+library or code object raises.
+
+``ManifestOp`` runs a manifest op description verbatim: it evaluates the grid
+expressions, packs the arguments by the launch's parameter kinds and calls
+``k3h_launch`` -- the path the kern runtime takes for a cubin, here for a
+gfx950 code object.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import struct
+from typing import Any, Sequence
+
+import torch  # loaded first: libk3h then binds to the HIP runtime torch already mapped
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+BUILD = os.path.join(PKG, "build")
+LIB_PATH = os.path.join(BUILD, "libk3h.so")
+
+K3H_OK, K3H_EINVAL, K3H_ENOMODULE, K3H_ENOENTRY, K3H_ENOMEM = 0, -1, -2, -3, -4
+
+MOE_V4 = "k3_moe_prefill_v4+EP_RANKS=4+EP_STRIDED=1+TILE_SHIFT=7+SCATTER_WARPS=16"
+MOE_V3 = "k3_moe_prefill_v3+EP_STRIDED=1"
+
+H = 7168
+
+
+class K3HError(RuntimeError):
+    def __init__(self, code: int, what: str):
+        self.code = code
+        super().__init__(f"{what}: {error_string(code)} ({code})")
+
+
+_lib: ctypes.CDLL | None = None
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+
+# name -> argtypes (restype is int for all of them)
+_SIGS: dict[str, list] = {
+    "k3h_module_load": [_P, ctypes.c_size_t, ctypes.POINTER(_P)],
+    "k3h_module_load_file": [ctypes.c_char_p, ctypes.POINTER(_P)],
+    "k3h_function": [_P, ctypes.c_char_p, ctypes.POINTER(_P)],
+    "k3h_launch": [_P, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint32),
+                   ctypes.c_uint32, _P, _P, ctypes.c_size_t],
+    "k3h_module_unload": [_P],
+    "k3h_runtime_version": [ctypes.POINTER(_I)],
+    "k3h_ctx_create": [ctypes.c_char_p, ctypes.POINTER(_P)],
+    "k3h_ctx_destroy": [_P],
+    "k3h_ctx_function": [_P, ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_P)],
+    "k3h_land_add_attnres_rms": [_P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F],
+    "k3h_land_add_attnres_rms_nb": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I],
+    "k3h_attnres_rms": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F],
+    "k3h_land_add2": [_P, _P, _P, _P, _P, _P, _I, _I],
+    "k3h_moe_quant": [_P, _P, _P, _P, _P, _I, _I],
+    "k3h_residual_rms_mxfp8": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _I],
+}
+
+
+def lib() -> ctypes.CDLL:
+    """Load libk3h.so (raises if it was not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise FileNotFoundError(
+                f"{LIB_PATH} is missing: build it with `python kern-k3_amd/build.py`")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, args in _SIGS.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = _I
+        L.k3h_error_string.argtypes = [_I]
+        L.k3h_error_string.restype = ctypes.c_char_p
+        _lib = L
+    return _lib
+
+
+def error_string(code: int) -> str:
+    return lib().k3h_error_string(code).decode()
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != K3H_OK:
+        if rc == K3H_EINVAL:
+            raise ValueError(f"{what}: invalid argument (rejected by libk3h)")
+        raise K3HError(rc, what)
+
+
+# ---------------------------------------------------------------- tensor checks
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _dev(t: torch.Tensor, name: str, dtypes: Sequence[torch.dtype], numel: int | None = None,
+         align: int = 16) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name}: expected a torch tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name}: must be a GPU tensor (got {t.device})")
+    if t.dtype not in dtypes:
+        raise ValueError(f"{name}: dtype {t.dtype} not in {list(dtypes)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: must be contiguous")
+    if numel is not None and t.numel() < numel:
+        raise ValueError(f"{name}: needs at least {numel} elements, has {t.numel()}")
+    if t.data_ptr() % align:
+        raise ValueError(f"{name}: must be {align}-byte aligned")
+
+
+BF16 = (torch.bfloat16,)
+U8 = (torch.uint8, torch.float8_e4m3fn)
+F32 = (torch.float32,)
+I32 = (torch.int32,)
+I64 = (torch.int64,)
+
+
+def _stream(stream: Any) -> int | None:
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+class Ctx:
+    """A k3h context: code objects loaded on first use from ``codeobj_dir``."""
+
+    def __init__(self, codeobj_dir: str = BUILD):
+        self.L = lib()
+        h = _P()
+        _check(self.L.k3h_ctx_create(codeobj_dir.encode(), ctypes.byref(h)), "k3h_ctx_create")
+        self.h = h
+        self.dir = codeobj_dir
+
+    def close(self) -> None:
+        if self.h:
+            self.L.k3h_ctx_destroy(self.h)
+            self.h = None
+
+    def function(self, module_key: str, entry: str) -> int:
+        f = _P()
+        _check(self.L.k3h_ctx_function(self.h, module_key.encode(), entry.encode(), ctypes.byref(f)),
+               f"{module_key}:{entry}")
+        return f.value
+
+    # ------------------------------------------------------------ K1 family
+    def land_add_attnres_rms(self, partial, prefix, blocks, sw, gamma, prefix2, normed, nb: int,
+                             snapshot: int, B: int, eps: float = 1e-5, stream=None) -> None:
+        """kern_k3_land_add_attnres_rms (k3_residual_v2.cu:295); partial bf16 or f32."""
+        n = B * H
+        _dev(partial, "partial", BF16 + F32, n)
+        if not snapshot:
+            _dev(prefix, "prefix", BF16, n)
+        if nb > 0:
+            _dev(blocks, "blocks", BF16, B * 8 * H)
+            _dev(sw, "sw", F32, H)
+        _dev(gamma, "gamma", BF16, H)
+        _dev(prefix2, "prefix2", BF16, n)
+        _dev(normed, "normed", BF16, n)
+        _check(self.L.k3h_land_add_attnres_rms(
+            self.h, _stream(stream), int(partial.dtype == torch.bfloat16), _ptr(partial),
+            _ptr(prefix), _ptr(blocks), _ptr(sw), _ptr(gamma), _ptr(prefix2), _ptr(normed), nb,
+            snapshot, B, eps), "land_add_attnres_rms")
+
+    def land_add_attnres_rms_nb(self, partial, prefix, blocks, sw, gamma, prefix2, normed,
+                                nb: int, snapshot: int, B: int, stream=None) -> None:
+        """kern_k3_land_add_attnres_rms_nb{nb} (k3_residual_nb.cu:350-811), LAND_BF16."""
+        n = B * H
+        _dev(partial, "partial", BF16, n)
+        if not snapshot:
+            _dev(prefix, "prefix", BF16, n)
+        _dev(blocks, "blocks", BF16, B * 8 * H)
+        _dev(sw, "sw", F32, H)
+        _dev(gamma, "gamma", BF16, H)
+        _dev(prefix2, "prefix2", BF16, n)
+        _dev(normed, "normed", BF16, n)
+        _check(self.L.k3h_land_add_attnres_rms_nb(
+            self.h, _stream(stream), _ptr(partial), _ptr(prefix), _ptr(blocks), _ptr(sw),
+            _ptr(gamma), _ptr(prefix2), _ptr(normed), nb, snapshot, B), "land_add_attnres_rms_nb")
+
+    def attnres_rms(self, prefix, blocks, sw, gamma, normed, nb: int, snapshot: int, B: int,
+                    eps: float = 1e-5, stream=None) -> None:
+        """kern_k3_attnres_rms (k3_residual_v2.cu:260)."""
+        _dev(prefix, "prefix", BF16, B * H)
+        if nb > 0 or snapshot:
+            _dev(blocks, "blocks", BF16, B * 8 * H)
+        if nb > 0:
+            _dev(sw, "sw", F32, H)
+        _dev(gamma, "gamma", BF16, H)
+        _dev(normed, "normed", BF16, B * H)
+        _check(self.L.k3h_attnres_rms(self.h, _stream(stream), _ptr(prefix), _ptr(blocks),
+                                      _ptr(sw), _ptr(gamma), _ptr(normed), nb, snapshot, B, eps),
+               "attnres_rms")
+
+    def land_add2(self, p1, p2, prefix2, hidden, two: int, B: int, stream=None) -> None:
+        """kern_k3_land_add2 (k3_residual_v2.cu:349)."""
+        _dev(p1, "p1", F32, B * H)
+        if two:
+            _dev(p2, "p2", F32, B * H)
+        _dev(prefix2, "prefix2", BF16, B * H)
+        _dev(hidden, "hidden", BF16, B * H)
+        _check(self.L.k3h_land_add2(self.h, _stream(stream), _ptr(p1), _ptr(p2), _ptr(prefix2),
+                                    _ptr(hidden), two, B), "land_add2")
+
+    # ------------------------------------------------------------ MXFP8
+    def moe_quant(self, x, q, sf, rows: int, cols: int, stream=None) -> None:
+        """kern_k3_moe_quant (k3_moe_prefill_v4.cu:111): manifest op moe_quant."""
+        n = rows * cols
+        if n % 32:
+            raise ValueError("moe_quant: rows * cols must be a multiple of 32")
+        _dev(x, "x", BF16, n)
+        _dev(q, "q", U8, n, align=8)
+        _dev(sf, "sf", U8, n // 32, align=1)
+        _check(self.L.k3h_moe_quant(self.h, _stream(stream), _ptr(x), _ptr(q), _ptr(sf), rows,
+                                    cols), "moe_quant")
+
+    def residual_rms_mxfp8(self, x, residual, gamma, residual_out, q, sf, normed=None,
+                           eps: float = 1e-6, B: int | None = None, stream=None) -> None:
+        """Fused residual add + RMSNorm + MXFP8 (K1b nb=0 composed with moe_quant)."""
+        B = x.shape[0] if B is None else B
+        n = B * H
+        _dev(x, "x", BF16, n)
+        _dev(residual, "residual", BF16, n)
+        _dev(gamma, "gamma", BF16, H)
+        _dev(residual_out, "residual_out", BF16, n)
+        _dev(q, "q", U8, n, align=8)
+        _dev(sf, "sf", U8, n // 32, align=1)
+        if normed is not None:
+            _dev(normed, "normed", BF16, n)
+        _check(self.L.k3h_residual_rms_mxfp8(self.h, _stream(stream), _ptr(x), _ptr(residual),
+                                             _ptr(gamma), _ptr(residual_out), _ptr(q), _ptr(sf),
+                                             _ptr(normed), eps, B), "residual_rms_mxfp8")
+
+
+# ---------------------------------------------------------------- manifest ops
+def _eval_expr(e: Any, env: dict[str, int]) -> int:
+    """Grid expressions of the manifest: ints, variable names, ceil_div/mul/add."""
+    if isinstance(e, int):
+        return e
+    if isinstance(e, str):
+        return int(env[e])
+    if isinstance(e, dict) and len(e) == 1:
+        (op, args), = e.items()
+        v = [_eval_expr(a, env) for a in args]
+        if op == "ceil_div":
+            return -(-v[0] // v[1])
+        if op == "mul":
+            return v[0] * v[1]
+        if op == "add":
+            return v[0] + v[1]
+    raise ValueError(f"unsupported grid expression {e!r}")
+
+
+def pack_args(kinds: Sequence[str], values: Sequence[Any]) -> bytes:
+    """Pack launch arguments at natural alignment (buffers/state/i64: 8 B; i32/f32: 4 B)."""
+    out = bytearray()
+    for kind, v in zip(kinds, values):
+        k = kind.split()[-1]
+        if k.startswith("buffer") or k == "state":
+            fmt, al = "<Q", 8
+            v = 0 if v is None else (v.data_ptr() if isinstance(v, torch.Tensor) else int(v))
+        elif k == "i64":
+            fmt, al = "<q", 8
+        elif k == "i32":
+            fmt, al = "<i", 4
+        elif k == "f32":
+            fmt, al = "<f", 4
+        else:
+            raise ValueError(f"unsupported parameter kind {kind!r}")
+        out += b"\0" * ((-len(out)) % al)
+        out += struct.pack(fmt, v)
+    return bytes(out)
+
+
+class ManifestOp:
+    """One manifest op (``ops.<name>``) executed launch by launch through k3h_launch."""
+
+    def __init__(self, ctx: Ctx, name: str, spec: dict):
+        self.ctx, self.name, self.spec = ctx, name, spec
+        self.params = spec["params"]
+
+    def __call__(self, args: Sequence[Any], env: dict[str, int], stream=None) -> None:
+        if len(args) != len(self.params):
+            raise ValueError(f"{self.name}: {len(self.params)} arguments expected")
+        L = self.ctx.L
+        for ln in self.spec["impl"]["launches"]:
+            kinds = ln.get("params", self.params)
+            if "args" in ln:
+                vals = []
+                for a in ln["args"]:
+                    (k, v), = a.items()
+                    vals.append(args[v] if k == "param" else v)
+            else:
+                vals = list(args)
+            buf = pack_args(kinds, vals)
+            fn = self.ctx.function(ln["module"], ln["entry"])
+            grid = (ctypes.c_uint32 * 3)(*[_eval_expr(g, env) for g in ln["grid"]])
+            block = (ctypes.c_uint32 * 3)(*ln["block"])
+            cbuf = ctypes.create_string_buffer(buf, len(buf))
+            _check(L.k3h_launch(fn, grid, block, ln.get("shared_mem", 0), _stream(stream),
+                                ctypes.cast(cbuf, _P), len(buf)),
+                   f"{self.name}:{ln['entry']}")

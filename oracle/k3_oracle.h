@@ -1,0 +1,73 @@
+/* CPU oracle for the K3 prefill memory-bound op family.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker: it is loaded by the
+ * tests, by __graft_entry__.smoke() and by the CPU-baseline leg of bench.py,
+ * never by the product path (kern-k3_amd/), which runs only on the GPU.
+ *
+ * Each function restates the arithmetic of a reference kernel in plain C,
+ * citing the reference file:line it follows.  Floating-point operations are
+ * single IEEE f32 operations (compiled with -ffp-contract=off); a fused
+ * multiply-add appears only as an explicit fmaf, where the reference's
+ * compiler contracts `a += x * y`.  Reductions replay the reference's order
+ * (per-thread serial sums, 32-lane xor butterflies, fixed-order partials).
+ *
+ * Where the reference calls an approximate CUDA intrinsic, the oracle uses a
+ * correctly rounded or documented replacement, named in the function's
+ * comment:
+ *   rsqrtf(v)      -> 1.0f / sqrtf(v), both correctly rounded;
+ *   expf / __expf  -> k3o_expf, a Cody-Waite + degree-7 Taylor exp whose
+ *                     steps are all correctly rounded f32 operations;
+ *   e4m3 / bf16    -> exact OCP / IEEE round-to-nearest-even encoders.
+ *
+ * bf16 tensors are uint16_t bit patterns; e4m3 and E8M0 tensors are uint8_t.
+ */
+#ifndef K3_ORACLE_H
+#define K3_ORACLE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- numerics ---------------------------------------------------------- */
+float k3o_bf2f(uint16_t h);
+uint16_t k3o_f2bf(float f);
+uint8_t k3o_e4m3(float x);
+float k3o_e4m3_decode(uint8_t c);
+float k3o_expf(float x);
+float k3o_sigmoid(float x);
+int k3o_mx_exp(float amax);
+void k3o_f2bf_n(const float* x, uint16_t* y, size_t n);
+void k3o_e4m3_n(const float* x, uint8_t* y, size_t n);
+void k3o_expf_n(const float* x, float* y, size_t n);
+
+/* ---- K1 residual family (k3_residual_v2.cu) ---------------------------- */
+/* partial_bf16 or partial_f32 (exactly one non-null) selects LAND_BF16. */
+void k3o_land_add_attnres_rms(const uint16_t* partial_bf16, const float* partial_f32,
+                              const uint16_t* prefix, const uint16_t* blocks,
+                              const float* sw, const uint16_t* gamma, uint16_t* prefix2,
+                              uint16_t* normed, int nb, int snapshot, int B, float eps);
+void k3o_attnres_rms(const uint16_t* prefix, uint16_t* blocks, const float* sw,
+                     const uint16_t* gamma, uint16_t* normed, int nb, int snapshot, int B,
+                     float eps);
+void k3o_land_add2(const float* p1, const float* p2, const uint16_t* prefix2, uint16_t* hidden,
+                   int two, int B);
+
+/* ---- MXFP8 (k3_moe_prefill_v4.cu:111-140) and the fused op ------------- */
+void k3o_moe_quant(const uint16_t* x, uint8_t* q, uint8_t* sf, int rows, int cols);
+void k3o_residual_rms_mxfp8(const uint16_t* x, const uint16_t* residual, const uint16_t* gamma,
+                            uint16_t* residual_out, uint8_t* q, uint8_t* sf, uint16_t* normed,
+                            int B, float eps);
+
+/* ---- per-tensor fp8 pair (k3_quant_fp8_pair{,_v2}.cu) ------------------- */
+void k3o_quant_fp8_amax(const uint16_t* x, int n, float* partials, int nb_grid, int v2);
+void k3o_quant_fp8_apply(const uint16_t* x, uint8_t* y, int n, const float* partials, int nb,
+                         float* scale_out);
+
+int k3o_num_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,149 @@
+"""numpy front end of the C oracle (``libk3oracle.so``).
+
+TEST INFRASTRUCTURE ONLY: imported by ``tests/``, ``__graft_entry__.smoke()`` and
+the CPU-baseline leg of ``bench.py``; the product path never loads it.
+
+bf16 arrays are ``np.uint16`` bit patterns; e4m3 / E8M0 arrays ``np.uint8``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+ODIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(ODIR, "libk3oracle.so")
+H = 7168
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            subprocess.run(["make", "-s", "-C", ODIR], check=True)
+        _lib = ctypes.CDLL(LIB_PATH)
+        _lib.k3o_bf2f.restype = ctypes.c_float
+        _lib.k3o_bf2f.argtypes = [ctypes.c_uint16]
+        _lib.k3o_f2bf.restype = ctypes.c_uint16
+        _lib.k3o_f2bf.argtypes = [ctypes.c_float]
+        _lib.k3o_e4m3.restype = ctypes.c_uint8
+        _lib.k3o_e4m3.argtypes = [ctypes.c_float]
+        _lib.k3o_e4m3_decode.restype = ctypes.c_float
+        _lib.k3o_e4m3_decode.argtypes = [ctypes.c_uint8]
+        _lib.k3o_expf.restype = ctypes.c_float
+        _lib.k3o_expf.argtypes = [ctypes.c_float]
+        _lib.k3o_sigmoid.restype = ctypes.c_float
+        _lib.k3o_sigmoid.argtypes = [ctypes.c_float]
+        _lib.k3o_mx_exp.restype = ctypes.c_int
+        _lib.k3o_mx_exp.argtypes = [ctypes.c_float]
+        _lib.k3o_num_threads.restype = ctypes.c_int
+    return _lib
+
+
+def _p(a: np.ndarray | None):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be contiguous"
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def num_threads() -> int:
+    return lib().k3o_num_threads()
+
+
+# ---------------------------------------------------------------- numerics
+def bf16_to_f32(h: np.ndarray) -> np.ndarray:
+    return (h.astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(x.shape, np.uint16)
+    lib().k3o_f2bf_n(_p(x), _p(y), ctypes.c_size_t(x.size))
+    return y
+
+
+def e4m3(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(x.shape, np.uint8)
+    lib().k3o_e4m3_n(_p(x), _p(y), ctypes.c_size_t(x.size))
+    return y
+
+
+def e4m3_decode(c: np.ndarray) -> np.ndarray:
+    L = lib()
+    return np.array([L.k3o_e4m3_decode(int(v)) for v in c.ravel()], np.float32).reshape(c.shape)
+
+
+def expf(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().k3o_expf_n(_p(x), _p(y), ctypes.c_size_t(x.size))
+    return y
+
+
+def mx_exp(amax: float) -> int:
+    return lib().k3o_mx_exp(float(amax))
+
+
+# ---------------------------------------------------------------- K1 family
+def land_add_attnres_rms(partial, prefix, blocks, sw, gamma, nb, snapshot, B, eps=1e-5):
+    """Returns (prefix2, normed); partial uint16 (bf16) or float32."""
+    prefix2 = np.empty((B, H), np.uint16)
+    normed = np.empty((B, H), np.uint16)
+    bf = partial.dtype == np.uint16
+    lib().k3o_land_add_attnres_rms(
+        _p(partial) if bf else None, None if bf else _p(partial), _p(prefix), _p(blocks), _p(sw),
+        _p(gamma), _p(prefix2), _p(normed), nb, snapshot, B, ctypes.c_float(eps))
+    return prefix2, normed
+
+
+def attnres_rms(prefix, blocks, sw, gamma, nb, snapshot, B, eps=1e-5):
+    """Returns (blocks_out, normed); blocks is copied, not modified."""
+    blocks_out = None if blocks is None else blocks.copy()
+    normed = np.empty((B, H), np.uint16)
+    lib().k3o_attnres_rms(_p(prefix), _p(blocks_out), _p(sw), _p(gamma), _p(normed), nb, snapshot,
+                          B, ctypes.c_float(eps))
+    return blocks_out, normed
+
+
+def land_add2(p1, p2, prefix2, two, B):
+    hidden = np.empty((B, H), np.uint16)
+    lib().k3o_land_add2(_p(p1), _p(p2), _p(prefix2), _p(hidden), two, B)
+    return hidden
+
+
+# ---------------------------------------------------------------- MXFP8
+def moe_quant(x, rows, cols):
+    n = rows * cols
+    q = np.empty(n, np.uint8)
+    sf = np.empty(n // 32, np.uint8)
+    lib().k3o_moe_quant(_p(np.ascontiguousarray(x)), _p(q), _p(sf), rows, cols)
+    return q.reshape(rows, cols), sf.reshape(rows, cols // 32)
+
+
+def residual_rms_mxfp8(x, residual, gamma, B, eps=1e-6, want_normed=True):
+    res_out = np.empty((B, H), np.uint16)
+    q = np.empty((B, H), np.uint8)
+    sf = np.empty((B, H // 32), np.uint8)
+    normed = np.empty((B, H), np.uint16) if want_normed else None
+    lib().k3o_residual_rms_mxfp8(_p(x), _p(residual), _p(gamma), _p(res_out), _p(q), _p(sf),
+                                 _p(normed), B, ctypes.c_float(eps))
+    return res_out, q, sf, normed
+
+
+def quant_fp8_amax(x, n, nb_grid, v2=True):
+    partials = np.empty(nb_grid, np.float32)
+    lib().k3o_quant_fp8_amax(_p(x), n, _p(partials), nb_grid, int(v2))
+    return partials
+
+
+def quant_fp8_apply(x, n, partials, nb):
+    y = np.empty(n, np.uint8)
+    scale = np.empty(1, np.float32)
+    lib().k3o_quant_fp8_apply(_p(x), _p(y), n, _p(partials), nb, _p(scale))
+    return y, scale

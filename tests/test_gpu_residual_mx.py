@@ -1,0 +1,260 @@
+"""GPU parity: K1 residual family, MXFP8 quant and the fused residual + RMSNorm
++ MXFP8 op against the C oracle, through the k3h C-ABI.  Bar: bit-exact for
+every output (prefix2/hidden/blocks by construction; normed because kernel and
+oracle share the reduction order and a correctly rounded 1/sqrt; q/sf because
+the MX rule is exact)."""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import k3h
+import oracle as O
+from k3data import H, bf16_to_f32, from_dev, normal_bf16, rng, to_bf16, to_dev
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _eq(name, got, want):
+    got, want = np.asarray(got), np.asarray(want)
+    assert got.shape == want.shape, (name, got.shape, want.shape)
+    bad = np.flatnonzero(got.ravel() != want.ravel())
+    assert bad.size == 0, f"{name}: {bad.size} of {got.size} differ, first at {bad[:5]}"
+
+
+def _k1_inputs(seed, B, land="bf16"):
+    g = rng(seed)
+    prefix = normal_bf16(g, (B, H))
+    partial = normal_bf16(g, (B, H)) if land == "bf16" else g.standard_normal((B, H), dtype=np.float32)
+    blocks = normal_bf16(g, (B, 8, H), 0.0, 2.0)
+    sw = g.standard_normal(H, dtype=np.float32) * np.float32(0.05)
+    gamma = normal_bf16(g, (H,), 1.0, 0.1)
+    return prefix, partial, blocks, sw, gamma
+
+
+@pytest.mark.parametrize("eps", [1e-6, 1e-5])
+def test_k1b_config1_nb0(ctx, eps):
+    """Config 1: tokens 1024, hidden 7168, plain residual add + RMSNorm."""
+    B = 1024
+    _case(f"k1b nb0 B={B} eps={eps}")
+    prefix, partial, blocks, sw, gamma = _k1_inputs(100, B)
+    want_p2, want_n = O.land_add_attnres_rms(partial, prefix, None, None, gamma, 0, 0, B, eps)
+    d = {k: to_dev(v) for k, v in dict(prefix=prefix, partial=partial, blocks=blocks, gamma=gamma).items()}
+    sw_d = to_dev(sw)
+    p2 = torch.empty((B, H), dtype=torch.bfloat16, device="cuda")
+    nrm = torch.empty_like(p2)
+    ctx.land_add_attnres_rms(d["partial"], d["prefix"], d["blocks"], sw_d, d["gamma"], p2, nrm, 0, 0, B, eps)
+    torch.cuda.synchronize()
+    _eq("prefix2", from_dev(p2), want_p2)
+    _eq("normed", from_dev(nrm), want_n)
+
+
+@pytest.mark.parametrize("land", ["bf16", "f32"])
+@pytest.mark.parametrize("nb,snapshot", [(0, 1), (1, 0), (2, 0), (3, 1), (5, 0), (8, 0), (8, 1)])
+def test_k1b_mixing(ctx, land, nb, snapshot):
+    B = 24
+    _case(f"k1b land={land} nb={nb} snapshot={snapshot}")
+    prefix, partial, blocks, sw, gamma = _k1_inputs(200 + nb, B, land)
+    want_p2, want_n = O.land_add_attnres_rms(partial, prefix, blocks, sw, gamma, nb, snapshot, B)
+    p2 = torch.empty((B, H), dtype=torch.bfloat16, device="cuda")
+    nrm = torch.empty_like(p2)
+    ctx.land_add_attnres_rms(to_dev(partial), to_dev(prefix), to_dev(blocks), to_dev(sw),
+                             to_dev(gamma), p2, nrm, nb, snapshot, B)
+    torch.cuda.synchronize()
+    _eq("prefix2", from_dev(p2), want_p2)
+    _eq("normed", from_dev(nrm), want_n)
+
+
+@pytest.mark.parametrize("nb", range(1, 9))
+def test_k1b_per_nb_entries(ctx, nb):
+    B = 12
+    _case(f"k1b_nb{nb}")
+    prefix, partial, blocks, sw, gamma = _k1_inputs(300 + nb, B)
+    want_p2, want_n = O.land_add_attnres_rms(partial, prefix, blocks, sw, gamma, nb, 0, B)
+    p2 = torch.empty((B, H), dtype=torch.bfloat16, device="cuda")
+    nrm = torch.empty_like(p2)
+    ctx.land_add_attnres_rms_nb(to_dev(partial), to_dev(prefix), to_dev(blocks), to_dev(sw),
+                                to_dev(gamma), p2, nrm, nb, 0, B)
+    torch.cuda.synchronize()
+    _eq("prefix2", from_dev(p2), want_p2)
+    _eq("normed", from_dev(nrm), want_n)
+
+
+@pytest.mark.parametrize("nb,snapshot", [(0, 0), (0, 1), (3, 1), (7, 1), (8, 1), (4, 0)])
+def test_k1a_attnres_rms(ctx, nb, snapshot):
+    B = 10
+    _case(f"k1a nb={nb} snapshot={snapshot}")
+    prefix, _, blocks, sw, gamma = _k1_inputs(400 + nb, B)
+    want_blk, want_n = O.attnres_rms(prefix, blocks, sw, gamma, nb, snapshot, B)
+    blk_d = to_dev(blocks)
+    nrm = torch.empty((B, H), dtype=torch.bfloat16, device="cuda")
+    ctx.attnres_rms(to_dev(prefix), blk_d, to_dev(sw), to_dev(gamma), nrm, nb, snapshot, B)
+    torch.cuda.synchronize()
+    _eq("blocks", from_dev(blk_d), want_blk)
+    _eq("normed", from_dev(nrm), want_n)
+
+
+@pytest.mark.parametrize("two", [0, 1])
+def test_k1c_land_add2(ctx, two):
+    B = 33
+    _case(f"k1c two={two}")
+    g = rng(500 + two)
+    p1 = g.standard_normal((B, H), dtype=np.float32) * np.float32(3)
+    p2 = g.standard_normal((B, H), dtype=np.float32)
+    prefix2 = normal_bf16(g, (B, H))
+    want = O.land_add2(p1, p2, prefix2, two, B)
+    hid = torch.empty((B, H), dtype=torch.bfloat16, device="cuda")
+    ctx.land_add2(to_dev(p1), to_dev(p2), to_dev(prefix2), hid, two, B)
+    torch.cuda.synchronize()
+    _eq("hidden", from_dev(hid), want)
+
+
+def _run_moe_quant(ctx, x, rows, cols):
+    q = torch.empty(rows * cols, dtype=torch.uint8, device="cuda")
+    sf = torch.empty(rows * cols // 32, dtype=torch.uint8, device="cuda")
+    ctx.moe_quant(to_dev(x), q, sf, rows, cols)
+    torch.cuda.synchronize()
+    return from_dev(q), from_dev(sf)
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 3584), (1024, 7168), (3, 7168), (1, 32), (7, 96)])
+def test_moe_quant(ctx, rows, cols):
+    _case(f"moe_quant {rows}x{cols}")
+    g = rng(600 + rows)
+    x = normal_bf16(g, (rows, cols), outlier_p=0.001)
+    x.reshape(-1)[:32] = 0
+    wq, wsf = O.moe_quant(x, rows, cols)
+    q, sf = _run_moe_quant(ctx, x, rows, cols)
+    _eq("sf", sf, wsf.reshape(-1))
+    _eq("q", q, wq.reshape(-1))
+
+
+def test_moe_quant_every_bf16_pattern(ctx):
+    """All 65536 bf16 patterns (NaN excluded) in shuffled 32-value blocks, plus
+    blocks holding +-inf: exercises the hardware e4m3 conversion over every
+    input and many block scales."""
+    _case("moe_quant all bf16 patterns")
+    g = rng(700)
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    f = bf16_to_f32(h)
+    h = h[~np.isnan(f)]
+    reps = []
+    for k in range(4):
+        reps.append(h[g.permutation(h.size)])
+    h = np.concatenate(reps)
+    h = h[: (h.size // 32) * 32]
+    rows = h.size // 32
+    wq, wsf = O.moe_quant(h, rows, 32)
+    q, sf = _run_moe_quant(ctx, h, rows, 32)
+    _eq("sf", sf, wsf.reshape(-1))
+    _eq("q", q, wq.reshape(-1))
+
+
+def _fused(ctx, x, res, gamma, B, eps, want_normed=True):
+    xd, rd, gd = to_dev(x), to_dev(res), to_dev(gamma)
+    ro = torch.empty((B, H), dtype=torch.bfloat16, device="cuda")
+    q = torch.empty((B, H), dtype=torch.uint8, device="cuda")
+    sf = torch.empty((B, H // 32), dtype=torch.uint8, device="cuda")
+    nrm = torch.empty((B, H), dtype=torch.bfloat16, device="cuda") if want_normed else None
+    ctx.residual_rms_mxfp8(xd, rd, gd, ro, q, sf, nrm, eps=eps, B=B)
+    torch.cuda.synchronize()
+    return from_dev(ro), from_dev(q), from_dev(sf), (from_dev(nrm) if want_normed else None)
+
+
+@pytest.mark.parametrize("B", [1024, 16384])
+def test_fused_residual_rms_mxfp8(ctx, B):
+    """Config 2 (16384 x 7168, 0.1% outliers x50) and a 1024-row slice."""
+    _case(f"fused residual+rms+mxfp8 B={B}")
+    g = rng(800 + B)
+    x = normal_bf16(g, (B, H), outlier_p=0.001)
+    res = normal_bf16(g, (B, H))
+    gamma = normal_bf16(g, (H,), 1.0, 0.1)
+    wro, wq, wsf, wn = O.residual_rms_mxfp8(x, res, gamma, B, 1e-6)
+    ro, q, sf, nrm = _fused(ctx, x, res, gamma, B, 1e-6)
+    _eq("residual_out", ro, wro)
+    _eq("normed", nrm, wn)
+    _eq("sf", sf, wsf)
+    _eq("q", q, wq)
+    # q / sf are the MX rule applied to the kernel's own normed row
+    q2, sf2 = O.moe_quant(nrm, B, H)
+    _eq("q(normed)", q, q2)
+    _eq("sf(normed)", sf, sf2)
+    # without the optional normed output the other outputs are unchanged
+    ro3, q3, sf3, _ = _fused(ctx, x, res, gamma, B, 1e-6, want_normed=False)
+    _eq("residual_out (no normed)", ro3, wro)
+    _eq("q (no normed)", q3, wq)
+    _eq("sf (no normed)", sf3, wsf)
+
+
+@pytest.mark.parametrize("B", [1, 3, 7])
+def test_fused_ragged_rows_and_eps(ctx, B):
+    _case(f"fused ragged B={B}")
+    g = rng(900 + B)
+    x = normal_bf16(g, (B, H), outlier_p=0.01)
+    res = normal_bf16(g, (B, H))
+    gamma = normal_bf16(g, (H,), 1.0, 0.1)
+    for eps in (1e-6, 1e-5, 0.5):
+        wro, wq, wsf, wn = O.residual_rms_mxfp8(x, res, gamma, B, eps)
+        ro, q, sf, nrm = _fused(ctx, x, res, gamma, B, eps)
+        _eq("residual_out", ro, wro)
+        _eq("normed", nrm, wn)
+        _eq("q", q, wq)
+        _eq("sf", sf, wsf)
+
+
+def test_zero_rows_launch_nothing(ctx):
+    _case("B=0")
+    t = torch.zeros(16, dtype=torch.bfloat16, device="cuda")
+    u = torch.zeros(16, dtype=torch.uint8, device="cuda")
+    g = torch.zeros(H, dtype=torch.bfloat16, device="cuda")
+    ctx.residual_rms_mxfp8(t, t, g, t, u, u, None, eps=1e-6, B=0)
+    torch.cuda.synchronize()
+
+
+def test_manifest_ops_through_module_launch(ctx):
+    """The manifests' own op descriptions (parameter kinds, argument maps, grid
+    expressions) run unchanged through k3h_launch on the gfx950 code objects."""
+    ops = json.load(open(os.path.join(GOLDEN, "manifest_hot_ops.json")))
+    tokens = 4 * 40  # B = ceil(tokens / 4) = 40 rows
+    B = 40
+    env = {"tokens": tokens}
+    # moe_quant: cols is fixed at 3584 by the op's argument map
+    _case("manifest moe_quant")
+    g = rng(1000)
+    x = normal_bf16(g, (B, 3584), outlier_p=0.001)
+    q = torch.empty(B * 3584, dtype=torch.uint8, device="cuda")
+    sf = torch.empty(B * 112, dtype=torch.uint8, device="cuda")
+    k3h.ManifestOp(ctx, "moe_quant", ops["moe_quant"])([to_dev(x), q, sf, B], env)
+    torch.cuda.synchronize()
+    wq, wsf = O.moe_quant(x, B, 3584)
+    _eq("q", from_dev(q), wq.reshape(-1))
+    _eq("sf", from_dev(sf), wsf.reshape(-1))
+    # K1b (l0-bf16 land_add_attnres_rms_bf16_v2) and the nb1 entry of the default manifest
+    prefix, partial, blocks, sw, gamma = _k1_inputs(1001, B)
+    for op, nb in (("land_add_attnres_rms_bf16_v2", 2), ("land_add_attnres_rms_bf16_v2_nb1", 1)):
+        _case(f"manifest {op}")
+        p2 = torch.empty((B, H), dtype=torch.bfloat16, device="cuda")
+        nrm = torch.empty_like(p2)
+        args = [to_dev(partial), to_dev(prefix), to_dev(blocks), to_dev(sw), to_dev(gamma), p2, nrm,
+                nb, 0, B]
+        k3h.ManifestOp(ctx, op, ops[op])(args, env)
+        torch.cuda.synchronize()
+        wp2, wn = O.land_add_attnres_rms(partial, prefix, blocks, sw, gamma, nb, 0, B)
+        _eq(f"{op} prefix2", from_dev(p2), wp2)
+        _eq(f"{op} normed", from_dev(nrm), wn)
+    # an nb entry called with another candidate count writes nothing
+    _case("manifest nb1 entry with nb_in=2")
+    p2 = torch.zeros((B, H), dtype=torch.bfloat16, device="cuda")
+    nrm = torch.zeros_like(p2)
+    args = [to_dev(partial), to_dev(prefix), to_dev(blocks), to_dev(sw), to_dev(gamma), p2, nrm, 2, 0, B]
+    k3h.ManifestOp(ctx, "land_add_attnres_rms_bf16_v2_nb1", ops["land_add_attnres_rms_bf16_v2_nb1"])(args, env)
+    torch.cuda.synchronize()
+    assert not from_dev(p2).any() and not from_dev(nrm).any()
