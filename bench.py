@@ -88,6 +88,28 @@ def cpu_baseline(x, res, gamma, gpu_out, budget_s: float = 10.0) -> dict:
     }
 
 
+def copy_ceiling(ctx, rows: int, reps: int) -> float:
+    """Rate of the plain 16-byte streaming copy over one [rows, 7168] bf16 tensor."""
+    import torch
+    src = torch.empty(rows * H, dtype=torch.bfloat16, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    s = torch.cuda.current_stream()
+    for _ in range(3):
+        ctx.stream_copy(src, dst, stream=s)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(reps):
+        ctx.stream_copy(src, dst, stream=s)
+    e1.record(s)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    gbs = 2 * src.numel() * 2 / (us * 1e-6) / 1e9
+    log(f"copy ceiling: {us:.1f} us per {2 * src.numel() * 2 / 1e6:.0f} MB -> {gbs:.0f} GB/s")
+    del src, dst
+    return gbs
+
+
 def load_traffic(kernel: str, workload: str):
     p = os.path.join(REPO, "profiles", "traffic.json")
     try:
@@ -105,6 +127,8 @@ def main() -> int:
     ap.add_argument("--rows", type=int, default=T)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--op", choices=["fused", "copy"], default="fused",
+                    help="copy: only the 16-byte streaming copy (counter calibration)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only (asked for {a.gpus}); the op family shards "
@@ -116,6 +140,11 @@ def main() -> int:
 
     ctx = k3h.Ctx()
     rows = a.rows
+    copy_gbs = copy_ceiling(ctx, rows, a.steps if a.op == "copy" else 20)
+    if a.op == "copy":
+        print(json.dumps({"op": "k3h_stream_copy", "bytes_per_launch": 2 * rows * H * 2,
+                          "gbs": round(copy_gbs, 1)}), flush=True)
+        return 0
     log(f"inputs {rows}x{H} bf16 on {torch.cuda.get_device_name(0)}")
     x, res, gamma = make_inputs(rows)
     ro = torch.empty_like(x)
@@ -144,7 +173,7 @@ def main() -> int:
     roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_GBS, "unit": "GB/s",
             "frac": round(gbs / PEAK_GBS, 4), "traffic": traffic,
             "kernel": "k3h_residual_rms_mxfp8", "algorithmic_bytes": nbytes,
-            "avg_launch_us": round(ms * 1e3, 2)}
+            "avg_launch_us": round(ms * 1e3, 2), "copy_ceiling_gbs": round(copy_gbs, 1)}
     cpu = None
     if not a.no_cpu:
         log("CPU baseline: C oracle on the same inputs")

@@ -99,10 +99,20 @@ K3H_API int k3h_moe_quant(k3h_ctx_t ctx, void* stream, const void* x, void* q, v
 
 /* k3h_residual_rms_mxfp8: fused residual add + RMSNorm + MXFP8 (no single
  * reference entry: K1b at nb = 0 composed with kern_k3_moe_quant).  Module
- * k3h_fused; grid (B), block 128.  normed may be NULL. */
+ * k3h_fused; grid ceil(B/2), block 256 (two rows per workgroup).  normed may be
+ * NULL; sf must be 4-byte aligned. */
 K3H_API int k3h_residual_rms_mxfp8(k3h_ctx_t ctx, void* stream, const void* x,
                                    const void* residual, const void* gamma, void* residual_out,
                                    void* q, void* sf, void* normed, float eps, int B);
+
+/* ---- measurement support --------------------------------------------------
+ * k3h_stream_copy: dst[i] = src[i] for n16 16-byte vectors with non-temporal
+ * loads and stores, one vector per thread (module k3h_fused).  No reference
+ * counterpart: it is the plain copy kernel whose rate is the HBM streaming
+ * ceiling the operators are compared with, and whose known byte count
+ * calibrates the FETCH_SIZE / WRITE_SIZE counters. */
+K3H_API int k3h_stream_copy(k3h_ctx_t ctx, void* stream, const void* src, void* dst,
+                            int64_t n16);
 
 #ifdef __cplusplus
 }

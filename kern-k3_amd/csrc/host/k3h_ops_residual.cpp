@@ -127,15 +127,26 @@ K3H_API int k3h_residual_rms_mxfp8(k3h_ctx_t ctx, void* stream, const void* x,
                                    void* q, void* sf, void* normed, float eps, int B) {
   if (!ctx || B < 0 || !(eps > 0.0f)) return K3H_EINVAL;
   if (!k3h_okp(x, 16) || !k3h_okp(residual, 16) || !k3h_okp(gamma, 16) ||
-      !k3h_okp(residual_out, 16) || !k3h_okp(q, 8) || !k3h_okp(sf, 1))
+      !k3h_okp(residual_out, 16) || !k3h_okp(q, 8) || !k3h_okp(sf, 4))
     return K3H_EINVAL;
   if (normed && !k3h_aligned(normed, 16)) return K3H_EINVAL;
   if (B == 0) return K3H_OK;
   K3hArgs a;
   a.ptr(x).ptr(residual).ptr(gamma).ptr(residual_out).ptr(q).ptr(sf).ptr(normed);
   a.f32(eps).i32(B);
-  return k3h_run(ctx, "k3h_fused", "k3h_residual_rms_mxfp8", (uint32_t)B, 1, 1, kResThreads,
-                 stream, a);
+  // two rows per 256-thread workgroup
+  return k3h_run(ctx, "k3h_fused", "k3h_residual_rms_mxfp8", k3h_cdiv(B, 2), 1, 1,
+                 2 * kResThreads, stream, a);
+}
+
+K3H_API int k3h_stream_copy(k3h_ctx_t ctx, void* stream, const void* src, void* dst,
+                            int64_t n16) {
+  if (!ctx || n16 < 0) return K3H_EINVAL;
+  if (n16 == 0) return K3H_OK;
+  if (!k3h_okp(src, 16) || !k3h_okp(dst, 16) || n16 > (int64_t)0xffffffff * 256) return K3H_EINVAL;
+  K3hArgs a;
+  a.ptr(src).ptr(dst).i64(n16);
+  return k3h_run(ctx, "k3h_fused", "k3h_stream_copy", k3h_cdiv(n16, 256), 1, 1, 256, stream, a);
 }
 
 }  // extern "C"

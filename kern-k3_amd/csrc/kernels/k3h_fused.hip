@@ -1,7 +1,7 @@
 // Module k3h_fused: operators with no single reference entry.
 //
 //   k3h_residual_rms_mxfp8(x, residual, gamma, residual_out, q, sf, normed, eps, B)
-//       grid (B, 1, 1)   block (128, 1, 1)
+//       grid (ceil(B / 2), 1, 1)   block (256, 1, 1)
 //
 // Residual add + RMSNorm + MXFP8: the K1b landing with nb = 0 and snapshot = 0
 // (k3_residual_v2.cu:295-345 with the row body of 107-257 reduced to its RMS
@@ -15,33 +15,48 @@
 // test path uses it to check q/sf against the exact normed values).
 //
 // HBM traffic per row: 2 x 14336 B read, 14336 + 7168 + 224 B written (gamma
-// is 14 KB shared by all rows and stays in L2).  One row per workgroup, thread
-// t owns 16-byte vectors t + 128 v, so a 32-value MX block is the 16-byte
-// vectors of four consecutive lanes at the same v.
+// is 14 KB shared by all rows and stays in L2).  A 256-thread workgroup holds
+// two rows, one per 128-thread half; within a half, thread t owns the 16-byte
+// vectors t + 128 v of its row (the K1 ownership, so the sum of squares has the
+// K1 order), and a 32-value MX block is the vectors of four consecutive lanes
+// at the same v.  Two rows per workgroup streams at the rate of a plain
+// two-read / 1.5-write copy on MI355X, where one row per 128-thread workgroup
+// loses about 4%.  The E8M0 bytes of four quads are gathered into one lane and
+// stored as a word.  A half whose row is past B still takes part in the
+// workgroup barrier but loads and stores nothing.
 #include "k3_residual_row.h"
 #include "k3_mx.h"
 
-extern "C" __global__ void __launch_bounds__(K3_RES_THREADS) k3h_residual_rms_mxfp8(
+#define K3_FUSED_ROWS 2
+
+extern "C" __global__ void __launch_bounds__(K3_RES_THREADS * K3_FUSED_ROWS) k3h_residual_rms_mxfp8(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ residual,
     const uint16_t* __restrict__ gamma, uint16_t* __restrict__ residual_out,
     uint8_t* __restrict__ q, uint8_t* __restrict__ sf, uint16_t* __restrict__ normed,
     float eps, int B) {
-  __shared__ float s_red[K3_NHW];
-  const int b = blockIdx.x;
-  if (b >= B) return;
-  const int t = threadIdx.x;
-  const size_t row = (size_t)b * K3_H;
+  __shared__ float s_red[K3_FUSED_ROWS * K3_NHW];
+  const int half = threadIdx.x / K3_RES_THREADS;
+  const int t = threadIdx.x % K3_RES_THREADS;
+  const int b = blockIdx.x * K3_FUSED_ROWS + half;
+  const bool live = b < B;
+  const size_t row = (size_t)(live ? b : 0) * K3_H;
 
+  // Loads are unconditional (a dead half reads row 0, which exists because the
+  // grid only covers B >= 1): a predicated load would be compiled as a branch
+  // with a full wait per vector and lose the memory-level parallelism.
   k3_u4 pv[K3_KVPT];
 #pragma unroll
   for (int v = 0; v < K3_KVPT; ++v) {
     const size_t off = row + k3_vec_off(t, v);
     pv[v] = k3_add_land(k3_ld16_nt(residual + off), k3_ld16_nt(x + off));
   }
+  if (live) {
 #pragma unroll
-  for (int v = 0; v < K3_KVPT; ++v) k3_st16_nt(residual_out + row + k3_vec_off(t, v), pv[v]);
+    for (int v = 0; v < K3_KVPT; ++v) k3_st16_nt(residual_out + row + k3_vec_off(t, v), pv[v]);
+  }
 
-  const float tot = k3_block_sum128(k3_row_sumsq(pv), s_red, t);
+  const float tot = k3_block_sum128(k3_row_sumsq(pv), s_red + half * K3_NHW, t);
+  if (!live) return;  // no barrier follows
   const float r = k3_row_rscale(tot, eps);
 #pragma unroll
   for (int v = 0; v < K3_KVPT; ++v) {
@@ -52,9 +67,20 @@ extern "C" __global__ void __launch_bounds__(K3_RES_THREADS) k3h_residual_rms_mx
     for (int j = 0; j < 4; ++j)
       nv[j] = k3_mul_bf2(k3_pack_bf2(k3_bf_lo(pv[v][j]) * r, k3_bf_hi(pv[v][j]) * r), g[j]);
     k3_u2 qv;
-    const int e = k3_mx_quad(nv, &qv);
+    const uint32_t sfb = (uint32_t)(k3_mx_quad(nv, &qv) + 127);
     k3_st8_nt(q + row + u, qv);
-    if ((t & 3) == 0) sf[(size_t)b * (K3_H / 32) + (u >> 5)] = (uint8_t)(e + 127);
+    // lane 16m gathers the bytes of quads 4m .. 4m + 3 (lanes 16m + 4k)
+    const uint32_t w = sfb | (k3_swz_xor_u32<4>(sfb) << 8) | (k3_swz_xor_u32<8>(sfb) << 16) |
+                       (k3_swz_xor_u32<12>(sfb) << 24);
+    if ((t & 15) == 0) *(uint32_t*)(sf + (size_t)b * (K3_H / 32) + (u >> 5)) = w;
     if (normed) k3_st16(normed + row + u, nv);
   }
+}
+
+// Plain 16-byte streaming copy (measurement support: the HBM ceiling and the
+// byte-counter calibration).  grid ceil(n16 / 256), block 256.
+extern "C" __global__ void __launch_bounds__(256) k3h_stream_copy(
+    const k3_u4* __restrict__ src, k3_u4* __restrict__ dst, long long n16) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i < n16) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
 }

@@ -65,6 +65,7 @@ _SIGS: dict[str, list] = {
     "k3h_land_add2": [_P, _P, _P, _P, _P, _P, _I, _I],
     "k3h_moe_quant": [_P, _P, _P, _P, _P, _I, _I],
     "k3h_residual_rms_mxfp8": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _I],
+    "k3h_stream_copy": [_P, _P, _P, _P, ctypes.c_int64],
 }
 
 
@@ -235,12 +236,24 @@ class Ctx:
         _dev(gamma, "gamma", BF16, H)
         _dev(residual_out, "residual_out", BF16, n)
         _dev(q, "q", U8, n, align=8)
-        _dev(sf, "sf", U8, n // 32, align=1)
+        _dev(sf, "sf", U8, n // 32, align=4)
         if normed is not None:
             _dev(normed, "normed", BF16, n)
         _check(self.L.k3h_residual_rms_mxfp8(self.h, _stream(stream), _ptr(x), _ptr(residual),
                                              _ptr(gamma), _ptr(residual_out), _ptr(q), _ptr(sf),
                                              _ptr(normed), eps, B), "residual_rms_mxfp8")
+
+
+    # ------------------------------------------------------------ measurement
+    def stream_copy(self, src, dst, stream=None) -> None:
+        """dst <- src with 16-byte non-temporal loads/stores (the HBM copy ceiling)."""
+        nbytes = src.numel() * src.element_size()
+        if nbytes % 16 or dst.numel() * dst.element_size() < nbytes:
+            raise ValueError("stream_copy: size must be a multiple of 16 bytes and fit dst")
+        _dev(src, "src", (src.dtype,))
+        _dev(dst, "dst", (dst.dtype,))
+        _check(self.L.k3h_stream_copy(self.h, _stream(stream), _ptr(src), _ptr(dst), nbytes // 16),
+               "stream_copy")
 
 
 # ---------------------------------------------------------------- manifest ops
