@@ -97,6 +97,19 @@ K3H_API int k3h_land_add2(k3h_ctx_t ctx, void* stream, const float* p1, const fl
 K3H_API int k3h_moe_quant(k3h_ctx_t ctx, void* stream, const void* x, void* q, void* sf,
                           int rows, int cols);
 
+/* ---- per-tensor fp8 pair ---------------------------------------------------
+ * kern_quant_fp8_amax[_v2] + kern_quant_fp8_apply[_v2] (k3_quant_fp8_pair.cu:18,32;
+ * k3_quant_fp8_pair_v2.cu:42,63; manifest op quant_fp8_tensor, json:407194):
+ * partials[nb] f32 (scratch owned by the caller), scale_out[1] f32, y u8 [n].
+ * Both launches grid (nb), block 256; the manifest uses nb = 2048.  v2 != 0
+ * selects the _v2 module.  The amax and apply steps are also exported alone. */
+K3H_API int k3h_quant_fp8_amax(k3h_ctx_t ctx, void* stream, int v2, const void* x, int n,
+                               float* partials, int nb);
+K3H_API int k3h_quant_fp8_apply(k3h_ctx_t ctx, void* stream, int v2, const void* x, void* y,
+                                int n, const float* partials, int nb, float* scale_out);
+K3H_API int k3h_quant_fp8_tensor(k3h_ctx_t ctx, void* stream, int v2, const void* x, void* y,
+                                 float* scale_out, float* partials, int n, int nb);
+
 /* k3h_residual_rms_mxfp8: fused residual add + RMSNorm + MXFP8 (no single
  * reference entry: K1b at nb = 0 composed with kern_k3_moe_quant).  Module
  * k3h_fused; grid ceil(B/2), block 256 (two rows per workgroup).  normed may be

@@ -35,6 +35,13 @@ SOURCES = {
     "k3h_fused": "k3h_fused.hip",
     "k3_moe_prefill_v3": "k3_moe_prefill.hip",
     "k3_moe_prefill_v4": "k3_moe_prefill.hip",
+    "k3_quant_fp8_pair": "k3_quant_fp8_pair.hip",
+    "k3_quant_fp8_pair_v2": "k3_quant_fp8_pair.hip",
+}
+
+# defines implied by a base name that shares its source with another base
+IMPLIED = {
+    "k3_quant_fp8_pair_v2": ["-DK3_QUANT_V2=1"],
 }
 
 # Every module key the host library or the manifests may load.
@@ -47,6 +54,8 @@ MODULES = [
     "k3h_fused",
     "k3_moe_prefill_v3+EP_STRIDED=1",
     "k3_moe_prefill_v4+EP_RANKS=4+EP_STRIDED=1+TILE_SHIFT=7+SCATTER_WARPS=16",
+    "k3_quant_fp8_pair",
+    "k3_quant_fp8_pair_v2",
 ]
 
 DEVICE_FLAGS = [
@@ -57,7 +66,7 @@ DEVICE_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
-HOST_SOURCES = ["k3h_module.cpp", "k3h_ops_residual.cpp"]
+HOST_SOURCES = ["k3h_module.cpp", "k3h_ops_residual.cpp", "k3h_ops_quant.cpp"]
 
 
 def module_defines(key: str) -> tuple[str, list[str]]:
@@ -65,7 +74,7 @@ def module_defines(key: str) -> tuple[str, list[str]]:
     base = parts[0]
     if base not in SOURCES:
         raise KeyError(f"unknown module base {base!r} in {key!r}")
-    defs = []
+    defs = list(IMPLIED.get(base, []))
     for p in parts[1:]:
         if "=" not in p:
             raise ValueError(f"bad define {p!r} in module key {key!r}")

@@ -66,6 +66,9 @@ _SIGS: dict[str, list] = {
     "k3h_moe_quant": [_P, _P, _P, _P, _P, _I, _I],
     "k3h_residual_rms_mxfp8": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _I],
     "k3h_stream_copy": [_P, _P, _P, _P, ctypes.c_int64],
+    "k3h_quant_fp8_amax": [_P, _P, _I, _P, _I, _P, _I],
+    "k3h_quant_fp8_apply": [_P, _P, _I, _P, _P, _I, _P, _I, _P],
+    "k3h_quant_fp8_tensor": [_P, _P, _I, _P, _P, _P, _P, _I, _I],
 }
 
 
@@ -243,6 +246,25 @@ class Ctx:
                                              _ptr(gamma), _ptr(residual_out), _ptr(q), _ptr(sf),
                                              _ptr(normed), eps, B), "residual_rms_mxfp8")
 
+
+    # ------------------------------------------------------------ per-tensor fp8
+    def quant_fp8_tensor(self, x, y, scale_out, partials, n: int, v2: bool = True,
+                         stream=None) -> None:
+        """Manifest op quant_fp8_tensor (params x, y, scale_out, partials, n): amax + apply."""
+        nb = partials.numel()
+        _dev(x, "x", BF16, n)
+        _dev(y, "y", U8, n, align=8)
+        _dev(scale_out, "scale_out", F32, 1, align=4)
+        _dev(partials, "partials", F32, 1, align=4)
+        _check(self.L.k3h_quant_fp8_tensor(self.h, _stream(stream), int(v2), _ptr(x), _ptr(y),
+                                           _ptr(scale_out), _ptr(partials), n, nb),
+               "quant_fp8_tensor")
+
+    def quant_fp8_amax(self, x, n: int, partials, v2: bool = True, stream=None) -> None:
+        _dev(x, "x", BF16, n)
+        _dev(partials, "partials", F32, 1, align=4)
+        _check(self.L.k3h_quant_fp8_amax(self.h, _stream(stream), int(v2), _ptr(x), n,
+                                         _ptr(partials), partials.numel()), "quant_fp8_amax")
 
     # ------------------------------------------------------------ measurement
     def stream_copy(self, src, dst, stream=None) -> None:

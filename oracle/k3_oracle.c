@@ -49,7 +49,7 @@ void k3o_f2bf_n(const float* x, uint16_t* y, size_t n) {
  * double, where every scaling below is exact. */
 uint8_t k3o_e4m3(float x) {
   const uint8_t sign = (uint8_t)((fbits(x) >> 24) & 0x80u);
-  if (isnan(x)) return (uint8_t)(sign | 0x7f);
+  if (isnan(x)) return 0x7f; /* canonical NaN of the saturating conversion */
   const double a = fabs((double)x);
   if (a >= 448.0) return (uint8_t)(sign | 0x7e);
   if (a < 0x1p-6) {                       /* subnormal quantum 2^-9 */
