@@ -118,6 +118,52 @@ K3H_API int k3h_residual_rms_mxfp8(k3h_ctx_t ctx, void* stream, const void* x,
                                    const void* residual, const void* gamma, void* residual_out,
                                    void* q, void* sf, void* normed, float eps, int B);
 
+/* ---- MoE router (module k3_router_argmax[+TOPK=8]) ----------------------------
+ * kern_k3_router_topk (k3_router_argmax.cu:87; manifest op router_topk,
+ * json:404788): S f32 [B,224], bias f32 [224], rs bf16 [1] -> idx i32 [B,topk],
+ * wts f32 [B,topk].  grid (B), block 256.  topk 16 (manifest) or 8. */
+K3H_API int k3h_router_topk(k3h_ctx_t ctx, void* stream, int topk, const float* S,
+                            const float* bias, const void* rs, int* idx, float* wts, int B);
+/* kern_k3_argmax_f32_partial + _final (k3_router_argmax.cu:186,227; op
+ * argmax_f32_one): pmax/pidx [B*parts] scratch, out i64 [B]. */
+K3H_API int k3h_argmax_f32(k3h_ctx_t ctx, void* stream, const float* logits, float* pmax,
+                           int* pidx, long long* out, int B, int n, int parts);
+
+/* ---- EP routing (module k3_moe_prefill_v4+EP_RANKS=4+EP_STRIDED=1+TILE_SHIFT=7+
+ * SCATTER_WARPS=16[+TOPK=8]); experts placed strided: id % 4 == rank -> id / 4. */
+/* kern_k3_moe_route_count (k3_moe_prefill_v4.cu:142; op moe_route_count,
+ * json:404991): ids i32 [T,topk] -> blockcount i32 [ceil(T/256), E]. */
+K3H_API int k3h_moe_route_count(k3h_ctx_t ctx, void* stream, int topk, const int* ids, int T,
+                                int rank, int E, int* blockcount);
+/* kern_k3_moe_route_tables (k3_moe_prefill_v4.cu:159; op moe_route_tables,
+ * json:405046).  grid 1, block 1024; tile must be 128. */
+K3H_API int k3h_moe_route_tables(k3h_ctx_t ctx, void* stream, const int* blockcount, int blocks,
+                                 int E, int tile, int* blockoff, int* cta_batch, int* cta_limit,
+                                 int* num_non_exiting, int* total_padded, int* route_map);
+/* kern_k3_moe_route_scatter (k3_moe_prefill_v4.cu:205; op moe_route_scatter,
+ * json:405120): route_map i32 [total_padded] (inout), exp2perm i32 [T,topk]. */
+K3H_API int k3h_moe_route_scatter(k3h_ctx_t ctx, void* stream, int topk, const int* ids,
+                                  const int* blockoff, int T, int rank, int E, int* route_map,
+                                  int* exp2perm);
+/* kern_k3_moe_finalize (k3_moe_prefill_v4.cu:254; op moe_finalize, json:405686):
+ * fc2 bf16 [total_padded, cols], wts f32 [T,topk] -> out bf16 [T, cols].
+ * grid ceil(T/2), block 128; cols % 8 == 0. */
+K3H_API int k3h_moe_finalize(k3h_ctx_t ctx, void* stream, int topk, const void* fc2,
+                             const int* exp2perm, const float* wts, void* out, int T, int cols);
+/* k3h_moe_permute_mx: no reference entry (moe_fc1 gathers through route_map
+ * inside the GEMM, ops.moe_fc1 json:405185).  pq[r] = q[route_map[r]] (cols
+ * e4m3 bytes), psf[r] = sf[route_map[r]] (cols/32 E8M0 bytes) for
+ * r < *total_padded (a device value).  Persistent grid 2048 x 256; cols % 512 == 0. */
+K3H_API int k3h_moe_permute_mx(k3h_ctx_t ctx, void* stream, const void* q, const void* sf,
+                               const int* route_map, const int* total_padded, int cols, void* pq,
+                               void* psf);
+/* kern_k3_moe_w_shuffle / kern_k3_moe_sf_shuffle (k3_moe_prefill_v4.cu:310,320):
+ * load-time weight / scale layouts of the grouped GEMM. */
+K3H_API int k3h_moe_w_shuffle(k3h_ctx_t ctx, void* stream, const void* src, void* dst,
+                              int experts, int n, int row_bytes, int gated);
+K3H_API int k3h_moe_sf_shuffle(k3h_ctx_t ctx, void* stream, const void* src, void* dst,
+                               int experts, int n, int kg, int gated);
+
 /* ---- measurement support --------------------------------------------------
  * k3h_stream_copy: dst[i] = src[i] for n16 16-byte vectors with non-temporal
  * loads and stores, one vector per thread (module k3h_fused).  No reference

@@ -37,6 +37,7 @@ SOURCES = {
     "k3_moe_prefill_v4": "k3_moe_prefill.hip",
     "k3_quant_fp8_pair": "k3_quant_fp8_pair.hip",
     "k3_quant_fp8_pair_v2": "k3_quant_fp8_pair.hip",
+    "k3_router_argmax": "k3_router_argmax.hip",
 }
 
 # defines implied by a base name that shares its source with another base
@@ -54,8 +55,11 @@ MODULES = [
     "k3h_fused",
     "k3_moe_prefill_v3+EP_STRIDED=1",
     "k3_moe_prefill_v4+EP_RANKS=4+EP_STRIDED=1+TILE_SHIFT=7+SCATTER_WARPS=16",
+    "k3_moe_prefill_v4+EP_RANKS=4+EP_STRIDED=1+TILE_SHIFT=7+SCATTER_WARPS=16+TOPK=8",
     "k3_quant_fp8_pair",
     "k3_quant_fp8_pair_v2",
+    "k3_router_argmax",
+    "k3_router_argmax+TOPK=8",
 ]
 
 DEVICE_FLAGS = [
@@ -66,7 +70,7 @@ DEVICE_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
-HOST_SOURCES = ["k3h_module.cpp", "k3h_ops_residual.cpp", "k3h_ops_quant.cpp"]
+HOST_SOURCES = ["k3h_module.cpp", "k3h_ops_residual.cpp", "k3h_ops_quant.cpp", "k3h_ops_moe.cpp"]
 
 
 def module_defines(key: str) -> tuple[str, list[str]]:

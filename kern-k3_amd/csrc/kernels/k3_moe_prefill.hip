@@ -1,12 +1,41 @@
 // Module k3_moe_prefill_v{3,4}+...: the MoE prefill memory-bound family on gfx950.
 //
-//   kern_k3_moe_quant(x, q, sf, rows, cols)
-//       grid (ceil(rows * cols / 32 / 256), 1, 1)   block (256, 1, 1)
+//   kern_k3_moe_quant(x, q, sf, rows, cols)       grid ceil(rows*cols/32/256), block 256
+//   kern_k3_moe_route_count(ids, T, rank, E, blockcount)      grid ceil(T/256), block 256
+//   kern_k3_moe_route_tables(blockcount, blocks, E, tile, blockoff, cta_batch,
+//       cta_limit, num_non_exiting, total_padded, route_map)  grid 1, block 1024
+//   kern_k3_moe_route_scatter(ids, blockoff, T, rank, E, route_map, exp2perm)
+//                                                   grid ceil(T/256), block 32*SCATTER_WARPS
+//   kern_k3_moe_finalize(fc2, exp2perm, wts, out, T, cols)     grid ceil(T/2), block 128
+//   kern_k3_moe_w_shuffle(src, dst, experts, n, row_bytes, gated)
+//   kern_k3_moe_sf_shuffle(src, dst, experts, n, kg, gated)
 //
 // Entry names, parameter order and launch geometry are the reference module's
-// (k3_moe_prefill_v4.cu:27-67; manifest ops moe_quant, moe_route_count,
-// moe_route_tables, moe_route_scatter, moe_finalize).
+// (k3_moe_prefill_v4.cu:27-80; manifest ops moe_quant, moe_route_count,
+// moe_route_tables, moe_route_scatter, moe_finalize at k3-tp4-prefill-16k.json
+// 404926, 404991, 405046, 405120, 405686).  Defines as in the module keys:
+// TOPK (16), EP_RANKS (4), EP_STRIDED, TILE_SHIFT (tile = 1 << TILE_SHIFT,
+// otherwise the run-time `tile`), SCATTER_WARPS (block 32 * SCATTER_WARPS).
+//
+// Plus one operator with no reference entry (module key k3_moe_prefill_v4+...):
+//   k3h_moe_permute_mx(q, sf, route_map, total_padded, cols, pq, psf)
+//       persistent grid, block 256: pq[r] = q[route_map[r]], psf[r] = sf[route_map[r]]
+//       for r < *total_padded (the reference gathers these rows inside moe_fc1).
 #include "k3_mx.h"
+
+#ifndef TOPK
+#define TOPK 16
+#endif
+#ifndef EP_RANKS
+#define EP_RANKS 4
+#endif
+#ifndef SCATTER_WARPS
+#define SCATTER_WARPS 8
+#endif
+#define MAX_E 64
+#define ROUTE_BLOCK 256
+#define ROUTE_IDS (ROUTE_BLOCK * TOPK)  // expanded ids per routing block
+#define ROUTE_CHUNKS (ROUTE_IDS / 64)   // 64-id chunks per routing block
 
 // MXFP8 quantisation of a row-major bf16 tensor, 32-value blocks taken over the
 // flat element order (k3_moe_prefill_v4.cu:111-140): sf[i] is the E8M0 scale
@@ -39,4 +68,292 @@ extern "C" __global__ void __launch_bounds__(256) kern_k3_moe_quant(
       if ((l & 3) == 0) sf[blk] = (uint8_t)(e + 127);
     }
   }
+}
+
+// ---------------------------------------------------------------- EP routing
+// Local slot of a global expert id, or -1 when another rank owns it
+// (k3_moe_prefill_v4.cu:100-109).
+K3_DEV int k3_local_expert(int id, int rank, int E) {
+#ifdef EP_STRIDED
+  if (id % EP_RANKS != rank) return -1;
+  const int e = id / EP_RANKS;
+  return e < E ? e : -1;
+#else
+  const int e = id - rank * E;
+  return (e >= 0 && e < E) ? e : -1;
+#endif
+}
+
+// blockcount[b][e]: ids of local expert e among tokens [256 b, 256 b + 256)
+// (k3_moe_prefill_v4.cu:142-157).  LDS counters; a count is order-free.
+extern "C" __global__ void __launch_bounds__(ROUTE_BLOCK) kern_k3_moe_route_count(
+    const int* __restrict__ ids, int T, int rank, int E, int* __restrict__ blockcount) {
+  __shared__ int cnt[MAX_E];
+  if ((int)threadIdx.x < E) cnt[threadIdx.x] = 0;
+  __syncthreads();
+  const int t = blockIdx.x * ROUTE_BLOCK + threadIdx.x;
+  if (t < T) {
+#pragma unroll
+    for (int k = 0; k < TOPK; ++k) {
+      const int e = k3_local_expert(ids[(size_t)t * TOPK + k], rank, E);
+      if (e >= 0) atomicAdd(&cnt[e], 1);
+    }
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < E) blockcount[blockIdx.x * E + threadIdx.x] = cnt[threadIdx.x];
+}
+
+// Wave-wide inclusive prefix sum (Hillis-Steele over 64 lanes).
+K3_DEV int k3_wave_incl_scan(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int p = __shfl_up(v, o, 64);
+    if (lane >= o) v += p;
+  }
+  return v;
+}
+
+// Routing tables (k3_moe_prefill_v4.cu:159-203): count[e] = sum over blocks,
+// off = exclusive scan of ceil(count / tile) (CTA units), blockoff[b][e] =
+// tile off[e] + the expert's count in blocks before b, padding rows of an
+// expert's last tile route token 0, cta_batch / cta_limit per CTA index.
+// One workgroup of 16 waves: wave w owns experts w, w + 16, ... and scans the
+// per-block counts across its lanes 64 blocks at a time.
+extern "C" __global__ void __launch_bounds__(1024) kern_k3_moe_route_tables(
+    const int* __restrict__ blockcount, int blocks, int E, int tile, int* __restrict__ blockoff,
+    int* __restrict__ cta_batch, int* __restrict__ cta_limit, int* __restrict__ num_non_exiting,
+    int* __restrict__ total_padded, int* __restrict__ route_map) {
+  __shared__ int count[MAX_E], off[MAX_E + 1];
+#ifdef TILE_SHIFT
+  tile = 1 << TILE_SHIFT;
+#endif
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+  // pass 1: per-expert totals
+  for (int e = wave; e < E; e += nw) {
+    int run = 0;
+    for (int b0 = 0; b0 < blocks; b0 += 64) {
+      const int b = b0 + lane;
+      const int c = b < blocks ? blockcount[b * E + e] : 0;
+      run += __shfl(k3_wave_incl_scan(c), 63, 64);
+    }
+    if (lane == 0) count[e] = run;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int j = 0; j < E; ++j) { off[j] = run; run += (count[j] + tile - 1) / tile; }
+    off[E] = run;
+    num_non_exiting[0] = run;
+    total_padded[0] = run * tile;
+  }
+  __syncthreads();
+  // pass 2: blockoff (exclusive scan over blocks) and the padding rows
+  for (int e = wave; e < E; e += nw) {
+    int base = off[e] * tile;
+    for (int b0 = 0; b0 < blocks; b0 += 64) {
+      const int b = b0 + lane;
+      const int c = b < blocks ? blockcount[b * E + e] : 0;
+      const int incl = k3_wave_incl_scan(c);
+      if (b < blocks) blockoff[b * E + e] = base + incl - c;
+      base += __shfl(incl, 63, 64);
+    }
+    for (int r = off[e] * tile + count[e] + lane; r < off[e + 1] * tile; r += 64) route_map[r] = 0;
+  }
+  // CTA tables
+  for (int i = threadIdx.x; i < off[E]; i += blockDim.x) {
+    int j = 0;
+    while (off[j + 1] <= i) ++j;
+    cta_batch[i] = j;
+    const int lim = off[j] * tile + count[j];
+    cta_limit[i] = min((i + 1) * tile, lim);
+  }
+}
+
+// Peers of this lane among the active lanes of the wave holding the same value
+// (a ballot loop over the distinct values present).
+K3_DEV uint64_t k3_match_any(int v) {
+  uint64_t todo = __ballot(1), mine = 0;
+  while (todo) {
+    const int leader = __builtin_ctzll(todo);
+    const int lv = __shfl(v, leader, 64);
+    const uint64_t m = __ballot(v == lv) & todo;
+    if (v == lv) mine = m;
+    todo &= ~m;
+  }
+  return mine;
+}
+
+// Route scatter (k3_moe_prefill_v4.cu:205-252).  For the expanded id
+// idx = t TOPK + k of routing block b with local expert e, the permuted row is
+// blockoff[b][e] + #{idx' < idx in block b with expert e}: a stable counting
+// sort of the block's ids by local expert.  The block's ROUTE_IDS ids are cut
+// into 64-id chunks in idx order; a chunk's per-expert counts go to LDS, one
+// scan per expert over the chunks gives each chunk's base, and a lane adds its
+// rank among the chunk's lanes of the same expert.
+extern "C" __global__ void __launch_bounds__(32 * SCATTER_WARPS) kern_k3_moe_route_scatter(
+    const int* __restrict__ ids, const int* __restrict__ blockoff, int T, int rank, int E,
+    int* __restrict__ route_map, int* __restrict__ exp2perm) {
+  __shared__ int hist[ROUTE_CHUNKS][MAX_E];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+  constexpr int CPW = (ROUTE_CHUNKS + (32 * SCATTER_WARPS / 64) - 1) / (32 * SCATTER_WARPS / 64);
+  const long long base = (long long)blockIdx.x * ROUTE_IDS;
+  const long long nid = (long long)T * TOPK;
+  for (int i = threadIdx.x; i < ROUTE_CHUNKS * MAX_E; i += blockDim.x) hist[i / MAX_E][i % MAX_E] = 0;
+  __syncthreads();
+  int ex[CPW], rk[CPW];
+  const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+  for (int r = 0; r < CPW; ++r) {
+    const int c = wave + r * nw;
+    ex[r] = -1;
+    rk[r] = 0;
+    if (c < ROUTE_CHUNKS) {
+      const long long idx = base + c * 64 + lane;
+      const int e = idx < nid ? k3_local_expert(ids[idx], rank, E) : -1;
+      const uint64_t peers = k3_match_any(e);
+      ex[r] = e;
+      rk[r] = __builtin_popcountll(peers & below);
+      if (e >= 0 && rk[r] == 0) hist[c][e] = __builtin_popcountll(peers);
+    }
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < E) {
+    int run = 0;
+    for (int c = 0; c < ROUTE_CHUNKS; ++c) {
+      const int n = hist[c][threadIdx.x];
+      hist[c][threadIdx.x] = run;
+      run += n;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < CPW; ++r) {
+    const int c = wave + r * nw;
+    if (c >= ROUTE_CHUNKS) continue;
+    const long long idx = base + c * 64 + lane;
+    if (idx >= nid) continue;
+    const int e = ex[r];
+    if (e < 0) { exp2perm[idx] = -1; continue; }
+    const int row = blockoff[blockIdx.x * E + e] + hist[c][e] + rk[r];
+    route_map[row] = (int)(idx / TOPK);
+    exp2perm[idx] = row;
+  }
+}
+
+// Weighted finalize (k3_moe_prefill_v4.cu:254-302): out[t, c] = bf16(sum over k
+// ascending of wts[t][k] * f32(fc2[exp2perm[t TOPK + k], c])) over the local
+// slots, f32 accumulator from 0, one fma per term.  Manifest geometry: grid
+// ceil(T / 2), block 128, so each wave owns one token: lanes < TOPK read the
+// token's slots, a ballot compacts the local ones, and the wave walks the row
+// two 16-byte vectors per lane at a time.
+extern "C" __global__ void __launch_bounds__(128) kern_k3_moe_finalize(
+    const uint16_t* __restrict__ fc2, const int* __restrict__ exp2perm,
+    const float* __restrict__ wts, uint16_t* __restrict__ out, int T, int cols) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 2 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  int p = -1;
+  float w = 0.0f;
+  if (lane < TOPK) {
+    p = exp2perm[(size_t)t * TOPK + lane];
+    w = wts[(size_t)t * TOPK + lane];
+  }
+  const uint64_t live = __ballot(p >= 0);
+  const int n = __builtin_popcountll(live);
+  // compacted slot i = the i-th local k (ascending)
+  int srow[TOPK];
+  float sw[TOPK];
+  {
+    uint64_t m = live;
+#pragma unroll
+    for (int i = 0; i < TOPK; ++i) {
+      const int k = m ? __builtin_ctzll(m) : 0;
+      srow[i] = __shfl(p, k, 64);
+      sw[i] = __shfl(w, k, 64);
+      m &= m - 1;
+    }
+  }
+  const int nvec = cols >> 3;  // 16-byte vectors per row
+  uint16_t* __restrict__ orow = out + (size_t)t * cols;
+  for (int v0 = lane; v0 < nvec; v0 += 128) {
+    const int v1 = v0 + 64;
+    const bool has1 = v1 < nvec;
+    float a0[8], a1[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) { a0[j] = 0.0f; a1[j] = 0.0f; }
+    for (int i = 0; i < n; ++i) {
+      const uint16_t* src = fc2 + (size_t)srow[i] * cols;
+      const k3_u4 x0 = k3_ld16(src + (size_t)v0 * 8);
+      const k3_u4 x1 = has1 ? k3_ld16(src + (size_t)v1 * 8) : k3_u4{0, 0, 0, 0};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        a0[2 * j] = __builtin_fmaf(sw[i], k3_bf_lo(x0[j]), a0[2 * j]);
+        a0[2 * j + 1] = __builtin_fmaf(sw[i], k3_bf_hi(x0[j]), a0[2 * j + 1]);
+        a1[2 * j] = __builtin_fmaf(sw[i], k3_bf_lo(x1[j]), a1[2 * j]);
+        a1[2 * j + 1] = __builtin_fmaf(sw[i], k3_bf_hi(x1[j]), a1[2 * j + 1]);
+      }
+    }
+    k3_u4 o0, o1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      o0[j] = k3_pack_bf2(a0[2 * j], a0[2 * j + 1]);
+      o1[j] = k3_pack_bf2(a1[2 * j], a1[2 * j + 1]);
+    }
+    k3_st16_nt(orow + (size_t)v0 * 8, o0);
+    if (has1) k3_st16_nt(orow + (size_t)v1 * 8, o1);
+  }
+}
+
+// MXFP8 permute: rows of the token-major MXFP8 activation gathered into the
+// expert-contiguous order of route_map (padding rows carry token 0, as routed).
+// Persistent: each wave copies whole rows, r = wave id + k * waves in the grid,
+// until *total_padded; per row 7168 payload bytes (7 x 16 B per lane at cols
+// 7168) and cols / 32 scale bytes.  cols % 512 == 0.
+extern "C" __global__ void __launch_bounds__(256) k3h_moe_permute_mx(
+    const uint8_t* __restrict__ q, const uint8_t* __restrict__ sf, const int* __restrict__ route_map,
+    const int* __restrict__ total_padded, int cols, uint8_t* __restrict__ pq, uint8_t* __restrict__ psf) {
+  const int lane = threadIdx.x & 63;
+  const int nrows = total_padded[0];
+  const int nwaves = gridDim.x * (blockDim.x >> 6);
+  const int nv = cols >> 4;          // 16-byte payload vectors per row
+  const int sfb = cols >> 5;         // scale bytes per row
+  for (int r = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); r < nrows; r += nwaves) {
+    const int t = route_map[r];
+    const uint8_t* src = q + (size_t)t * cols;
+    uint8_t* dst = pq + (size_t)r * cols;
+    for (int v = lane; v < nv; v += 64) k3_st16_nt(dst + (size_t)v * 16, k3_ld16(src + (size_t)v * 16));
+    const uint8_t* ssrc = sf + (size_t)t * sfb;
+    uint8_t* sdst = psf + (size_t)r * sfb;
+    for (int i = lane * 4; i < sfb; i += 256) *(uint32_t*)(sdst + i) = *(const uint32_t*)(ssrc + i);
+  }
+}
+
+// Load-time weight layouts (k3_moe_prefill_v4.cu:69-80, 304-327): row r of each
+// expert's destination takes source row shuffle(r); scales also re-laid in
+// 128 x 4 blocks.
+K3_DEV int k3_w_shuffle_row(int r, int n, int gated) {
+  const int u = (r / 32) * 32 + (r % 8) * 4 + (r % 32) / 8;
+  return gated ? (u % 2 ? n / 2 : 0) + u / 2 : u;
+}
+
+extern "C" __global__ void __launch_bounds__(256) kern_k3_moe_w_shuffle(
+    const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int experts, int n, int row_bytes,
+    int gated) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int per_row = row_bytes / 16;
+  if (i >= (long long)experts * n * per_row) return;
+  const int c = (int)(i % per_row), r = (int)(i / per_row % n), e = (int)(i / per_row / n);
+  k3_st16(dst + i * 16, k3_ld16(src + ((long long)e * n + k3_w_shuffle_row(r, n, gated)) * row_bytes + (long long)c * 16));
+}
+
+extern "C" __global__ void __launch_bounds__(256) kern_k3_moe_sf_shuffle(
+    const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int experts, int n, int kg,
+    int gated) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long long)experts * n * kg) return;
+  const int c = (int)(i % kg), r = (int)(i / kg % n), e = (int)(i / kg / n);
+  const long long at = ((long long)(r / 128) * (kg / 4) + c / 4) * 512 + (r % 32) * 16 +
+                       ((r % 128) / 32) * 4 + c % 4;
+  dst[(long long)e * n * kg + at] = src[((long long)e * n + k3_w_shuffle_row(r, n, gated)) * kg + c];
 }

@@ -69,6 +69,15 @@ _SIGS: dict[str, list] = {
     "k3h_quant_fp8_amax": [_P, _P, _I, _P, _I, _P, _I],
     "k3h_quant_fp8_apply": [_P, _P, _I, _P, _P, _I, _P, _I, _P],
     "k3h_quant_fp8_tensor": [_P, _P, _I, _P, _P, _P, _P, _I, _I],
+    "k3h_router_topk": [_P, _P, _I, _P, _P, _P, _P, _P, _I],
+    "k3h_argmax_f32": [_P, _P, _P, _P, _P, _P, _I, _I, _I],
+    "k3h_moe_route_count": [_P, _P, _I, _P, _I, _I, _I, _P],
+    "k3h_moe_route_tables": [_P, _P, _P, _I, _I, _I, _P, _P, _P, _P, _P, _P],
+    "k3h_moe_route_scatter": [_P, _P, _I, _P, _P, _I, _I, _I, _P, _P],
+    "k3h_moe_finalize": [_P, _P, _I, _P, _P, _P, _P, _I, _I],
+    "k3h_moe_permute_mx": [_P, _P, _P, _P, _P, _P, _I, _P, _P],
+    "k3h_moe_w_shuffle": [_P, _P, _P, _P, _I, _I, _I, _I],
+    "k3h_moe_sf_shuffle": [_P, _P, _P, _P, _I, _I, _I, _I],
 }
 
 
@@ -265,6 +274,88 @@ class Ctx:
         _dev(partials, "partials", F32, 1, align=4)
         _check(self.L.k3h_quant_fp8_amax(self.h, _stream(stream), int(v2), _ptr(x), n,
                                          _ptr(partials), partials.numel()), "quant_fp8_amax")
+
+    # ------------------------------------------------------------ MoE router
+    def router_topk(self, S, bias, rs, idx, wts, B: int, topk: int = 16, stream=None) -> None:
+        """Manifest op router_topk (S, bias, rs, idx, wts, B) -- kern_k3_router_topk."""
+        _dev(S, "S", F32, B * 224, align=4)
+        _dev(bias, "bias", F32, 224, align=4)
+        _dev(rs, "rs", BF16, 1, align=2)
+        _dev(idx, "idx", I32, B * topk, align=4)
+        _dev(wts, "wts", F32, B * topk, align=4)
+        _check(self.L.k3h_router_topk(self.h, _stream(stream), topk, _ptr(S), _ptr(bias), _ptr(rs),
+                                      _ptr(idx), _ptr(wts), B), "router_topk")
+
+    def argmax_f32(self, logits, pmax, pidx, out, B: int, n: int, parts: int, stream=None) -> None:
+        _dev(logits, "logits", F32, B * n, align=4)
+        _dev(pmax, "pmax", F32, B * parts, align=4)
+        _dev(pidx, "pidx", I32, B * parts, align=4)
+        _dev(out, "out", I64, B, align=8)
+        _check(self.L.k3h_argmax_f32(self.h, _stream(stream), _ptr(logits), _ptr(pmax), _ptr(pidx),
+                                     _ptr(out), B, n, parts), "argmax_f32")
+
+    # ------------------------------------------------------------ EP routing
+    def moe_route_count(self, ids, T: int, rank: int, E: int, blockcount, topk: int = 16,
+                        stream=None) -> None:
+        _dev(ids, "ids", I32, T * topk, align=4)
+        _dev(blockcount, "blockcount", I32, -(-T // 256) * E, align=4)
+        _check(self.L.k3h_moe_route_count(self.h, _stream(stream), topk, _ptr(ids), T, rank, E,
+                                          _ptr(blockcount)), "moe_route_count")
+
+    def moe_route_tables(self, blockcount, blocks: int, E: int, tile: int, blockoff, cta_batch,
+                         cta_limit, num_non_exiting, total_padded, route_map, stream=None) -> None:
+        for nm, t in (("blockcount", blockcount), ("blockoff", blockoff), ("cta_batch", cta_batch),
+                      ("cta_limit", cta_limit), ("num_non_exiting", num_non_exiting),
+                      ("total_padded", total_padded), ("route_map", route_map)):
+            _dev(t, nm, I32, 1, align=4)
+        _check(self.L.k3h_moe_route_tables(self.h, _stream(stream), _ptr(blockcount), blocks, E, tile,
+                                           _ptr(blockoff), _ptr(cta_batch), _ptr(cta_limit),
+                                           _ptr(num_non_exiting), _ptr(total_padded),
+                                           _ptr(route_map)), "moe_route_tables")
+
+    def moe_route_scatter(self, ids, blockoff, T: int, rank: int, E: int, route_map, exp2perm,
+                          topk: int = 16, stream=None) -> None:
+        _dev(ids, "ids", I32, T * topk, align=4)
+        _dev(blockoff, "blockoff", I32, -(-T // 256) * E, align=4)
+        _dev(route_map, "route_map", I32, 1, align=4)
+        _dev(exp2perm, "exp2perm", I32, T * topk, align=4)
+        _check(self.L.k3h_moe_route_scatter(self.h, _stream(stream), topk, _ptr(ids), _ptr(blockoff),
+                                            T, rank, E, _ptr(route_map), _ptr(exp2perm)),
+               "moe_route_scatter")
+
+    def moe_finalize(self, fc2, exp2perm, wts, out, T: int, cols: int, topk: int = 16,
+                     stream=None) -> None:
+        _dev(fc2, "fc2", BF16, cols)
+        _dev(exp2perm, "exp2perm", I32, T * topk, align=4)
+        _dev(wts, "wts", F32, T * topk, align=4)
+        _dev(out, "out", BF16, T * cols)
+        _check(self.L.k3h_moe_finalize(self.h, _stream(stream), topk, _ptr(fc2), _ptr(exp2perm),
+                                       _ptr(wts), _ptr(out), T, cols), "moe_finalize")
+
+    def moe_permute_mx(self, q, sf, route_map, total_padded, cols: int, pq, psf, stream=None) -> None:
+        _dev(q, "q", U8, cols)
+        _dev(sf, "sf", U8, cols // 32, align=4)
+        _dev(route_map, "route_map", I32, 1, align=4)
+        _dev(total_padded, "total_padded", I32, 1, align=4)
+        _dev(pq, "pq", U8, cols)
+        _dev(psf, "psf", U8, cols // 32, align=4)
+        _check(self.L.k3h_moe_permute_mx(self.h, _stream(stream), _ptr(q), _ptr(sf), _ptr(route_map),
+                                         _ptr(total_padded), cols, _ptr(pq), _ptr(psf)),
+               "moe_permute_mx")
+
+    def moe_w_shuffle(self, src, dst, experts: int, n: int, row_bytes: int, gated: int,
+                      stream=None) -> None:
+        _dev(src, "src", U8, experts * n * row_bytes)
+        _dev(dst, "dst", U8, experts * n * row_bytes)
+        _check(self.L.k3h_moe_w_shuffle(self.h, _stream(stream), _ptr(src), _ptr(dst), experts, n,
+                                        row_bytes, gated), "moe_w_shuffle")
+
+    def moe_sf_shuffle(self, src, dst, experts: int, n: int, kg: int, gated: int,
+                       stream=None) -> None:
+        _dev(src, "src", U8, experts * n * kg, align=1)
+        _dev(dst, "dst", U8, experts * n * kg, align=1)
+        _check(self.L.k3h_moe_sf_shuffle(self.h, _stream(stream), _ptr(src), _ptr(dst), experts, n,
+                                         kg, gated), "moe_sf_shuffle")
 
     # ------------------------------------------------------------ measurement
     def stream_copy(self, src, dst, stream=None) -> None:

@@ -65,6 +65,31 @@ void k3o_quant_fp8_amax(const uint16_t* x, int n, float* partials, int nb_grid, 
 void k3o_quant_fp8_apply(const uint16_t* x, uint8_t* y, int n, const float* partials, int nb,
                          float* scale_out);
 
+/* ---- router / argmax (k3_router_argmax.cu) ------------------------------ */
+uint32_t k3o_ord_f32(float f);
+void k3o_sigmoid_n(const float* x, float* y, size_t n);
+void k3o_router_topk(const float* S, const float* bias, const uint16_t* rs, int* idx, float* wts,
+                     int B, int topk);
+void k3o_argmax_partial(const float* logits, float* pmax, int* pidx, int B, int n, int parts);
+void k3o_argmax_final(const float* pmax, const int* pidx, long long* out, int B, int parts);
+
+/* ---- EP routing, permute, finalize, weight layouts (k3_moe_prefill_v4.cu) -- */
+int k3o_local_expert(int id, int rank, int E, int ep_ranks, int strided);
+void k3o_route_count(const int* ids, int T, int topk, int rank, int E, int ep_ranks, int strided,
+                     int* blockcount);
+void k3o_route_tables(const int* blockcount, int blocks, int E, int tile, int* blockoff,
+                      int* cta_batch, int* cta_limit, int* num_non_exiting, int* total_padded,
+                      int* route_map);
+void k3o_route_scatter(const int* ids, const int* blockoff, int T, int topk, int rank, int E,
+                       int ep_ranks, int strided, int* route_map, int* exp2perm);
+void k3o_moe_permute_mx(const uint8_t* q, const uint8_t* sf, const int* route_map,
+                        int total_padded, int cols, uint8_t* pq, uint8_t* psf);
+void k3o_moe_finalize(const uint16_t* fc2, const int* exp2perm, const float* wts, uint16_t* out,
+                      int T, int topk, int cols);
+void k3o_moe_w_shuffle(const uint8_t* src, uint8_t* dst, int experts, int n, int row_bytes,
+                       int gated);
+void k3o_moe_sf_shuffle(const uint8_t* src, uint8_t* dst, int experts, int n, int kg, int gated);
+
 int k3o_num_threads(void);
 
 #ifdef __cplusplus

@@ -147,3 +147,96 @@ def quant_fp8_apply(x, n, partials, nb):
     scale = np.empty(1, np.float32)
     lib().k3o_quant_fp8_apply(_p(x), _p(y), n, _p(partials), nb, _p(scale))
     return y, scale
+
+
+# ---------------------------------------------------------------- router / argmax
+def sigmoid(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().k3o_sigmoid_n(_p(x), _p(y), ctypes.c_size_t(x.size))
+    return y
+
+
+def router_topk(S, bias, rs_bf16, B, topk):
+    idx = np.empty((B, topk), np.int32)
+    wts = np.empty((B, topk), np.float32)
+    rs = np.ascontiguousarray(np.array([rs_bf16], np.uint16).reshape(-1)[:1])
+    lib().k3o_router_topk(_p(np.ascontiguousarray(S, np.float32)), _p(np.ascontiguousarray(bias, np.float32)),
+                          _p(rs), _p(idx), _p(wts), B, topk)
+    return idx, wts
+
+
+def argmax_partial(logits, B, n, parts):
+    pmax = np.empty(B * parts, np.float32)
+    pidx = np.empty(B * parts, np.int32)
+    lib().k3o_argmax_partial(_p(np.ascontiguousarray(logits, np.float32)), _p(pmax), _p(pidx), B, n, parts)
+    return pmax, pidx
+
+
+def argmax_final(pmax, pidx, B, parts):
+    out = np.empty(B, np.int64)
+    lib().k3o_argmax_final(_p(pmax), _p(pidx), _p(out), B, parts)
+    return out
+
+
+# ---------------------------------------------------------------- EP routing
+def local_expert(i, rank, E, ep_ranks=4, strided=1):
+    return lib().k3o_local_expert(int(i), rank, E, ep_ranks, strided)
+
+
+def route_count(ids, T, topk, rank, E, ep_ranks=4, strided=1):
+    nblk = (T + 255) // 256
+    bc = np.empty(nblk * E, np.int32)
+    lib().k3o_route_count(_p(np.ascontiguousarray(ids, np.int32)), T, topk, rank, E, ep_ranks, strided, _p(bc))
+    return bc
+
+
+def route_tables(blockcount, blocks, E, tile, route_map_len):
+    """Returns dict of blockoff, cta_batch, cta_limit, num_non_exiting, total_padded and
+    route_map (padding rows only; other rows -1 sentinel as the oracle leaves them)."""
+    blockoff = np.empty(blocks * E, np.int32)
+    nmax = route_map_len // tile + 1
+    cta_batch = np.full(nmax, -1, np.int32)
+    cta_limit = np.full(nmax, -1, np.int32)
+    nne = np.zeros(1, np.int32)
+    tp = np.zeros(1, np.int32)
+    rmap = np.full(route_map_len, -1, np.int32)
+    lib().k3o_route_tables(_p(np.ascontiguousarray(blockcount, np.int32)), blocks, E, tile, _p(blockoff),
+                           _p(cta_batch), _p(cta_limit), _p(nne), _p(tp), _p(rmap))
+    return dict(blockoff=blockoff, cta_batch=cta_batch, cta_limit=cta_limit,
+                num_non_exiting=int(nne[0]), total_padded=int(tp[0]), route_map=rmap)
+
+
+def route_scatter(ids, blockoff, T, topk, rank, E, route_map, ep_ranks=4, strided=1):
+    rmap = route_map.copy()
+    e2p = np.empty(T * topk, np.int32)
+    lib().k3o_route_scatter(_p(np.ascontiguousarray(ids, np.int32)), _p(blockoff), T, topk, rank, E,
+                            ep_ranks, strided, _p(rmap), _p(e2p))
+    return rmap, e2p
+
+
+def moe_permute_mx(q, sf, route_map, total_padded, cols):
+    pq = np.empty((total_padded, cols), np.uint8)
+    psf = np.empty((total_padded, cols // 32), np.uint8)
+    lib().k3o_moe_permute_mx(_p(np.ascontiguousarray(q)), _p(np.ascontiguousarray(sf)),
+                             _p(np.ascontiguousarray(route_map, np.int32)), total_padded, cols, _p(pq), _p(psf))
+    return pq, psf
+
+
+def moe_finalize(fc2, exp2perm, wts, T, topk, cols):
+    out = np.empty((T, cols), np.uint16)
+    lib().k3o_moe_finalize(_p(np.ascontiguousarray(fc2)), _p(np.ascontiguousarray(exp2perm, np.int32)),
+                           _p(np.ascontiguousarray(wts, np.float32)), _p(out), T, topk, cols)
+    return out
+
+
+def moe_w_shuffle(src, experts, n, row_bytes, gated):
+    dst = np.empty_like(src)
+    lib().k3o_moe_w_shuffle(_p(src), _p(dst), experts, n, row_bytes, gated)
+    return dst
+
+
+def moe_sf_shuffle(src, experts, n, kg, gated):
+    dst = np.empty_like(src)
+    lib().k3o_moe_sf_shuffle(_p(src), _p(dst), experts, n, kg, gated)
+    return dst

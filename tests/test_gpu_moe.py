@@ -1,0 +1,232 @@
+"""GPU parity: router top-k, argmax, EP routing tables, MXFP8 permute, weighted
+finalize and the weight layouts against the C oracle -- bit-exact for indices,
+weights, every routing table, permuted bytes and the finalize output (both
+sides use the same fma order)."""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import k3h
+import oracle as O
+from k3data import from_dev, normal_bf16, rng, to_bf16, to_dev
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+E, RANK = 56, 0
+
+
+def _case(m):
+    print(f"[case] {m}", flush=True)
+
+
+def _eq(name, got, want):
+    got, want = np.asarray(got), np.asarray(want)
+    assert got.shape == want.shape, (name, got.shape, want.shape)
+    bad = np.flatnonzero(got.ravel() != want.ravel())
+    assert bad.size == 0, f"{name}: {bad.size} of {got.size} differ, first at {bad[:5]}"
+
+
+def _router_inputs(T, seed):
+    g = rng(seed)
+    S = g.standard_normal((T, 224), dtype=np.float32)
+    S[0, 10:20] = S[0, 5]
+    bias = (g.standard_normal(224) * 0.01).astype(np.float32)
+    bias[10:20] = bias[5]
+    rs = to_bf16(np.array([2.5], np.float32))
+    return S, bias, rs
+
+
+def _run_router(ctx, S, bias, rs, T, topk):
+    idx = torch.empty((T, topk), dtype=torch.int32, device="cuda")
+    wts = torch.empty((T, topk), dtype=torch.float32, device="cuda")
+    ctx.router_topk(to_dev(S), to_dev(bias), to_dev(rs), idx, wts, T, topk=topk)
+    torch.cuda.synchronize()
+    return from_dev(idx), from_dev(wts)
+
+
+@pytest.mark.parametrize("T,topk", [(16384, 8), (4096, 16), (1, 16), (5, 8)])
+def test_router_topk(ctx, T, topk):
+    _case(f"router_topk T={T} topk={topk}")
+    S, bias, rs = _router_inputs(T, 1300 + T)
+    want_i, want_w = O.router_topk(S, bias, rs[0], T, topk)
+    idx, wts = _run_router(ctx, S, bias, rs, T, topk)
+    _eq("idx", idx, want_i)
+    _eq("wts", wts.view(np.uint32), want_w.view(np.uint32))
+
+
+def test_argmax_f32(ctx):
+    _case("argmax")
+    g = rng(1400)
+    B, n, parts = 16, 163840, 64
+    x = g.standard_normal((B, n), dtype=np.float32)
+    x[1, 100] = x[1, 150000] = 9.0
+    x[2, :] = -np.inf
+    x[3, 77] = np.inf
+    pm, pi = O.argmax_partial(x, B, n, parts)
+    out = O.argmax_final(pm, pi, B, parts)
+    d_pm = torch.empty(B * parts, dtype=torch.float32, device="cuda")
+    d_pi = torch.empty(B * parts, dtype=torch.int32, device="cuda")
+    d_out = torch.empty(B, dtype=torch.int64, device="cuda")
+    ctx.argmax_f32(to_dev(x), d_pm, d_pi, d_out, B, n, parts)
+    torch.cuda.synchronize()
+    _eq("pmax", from_dev(d_pm).view(np.uint32), pm.view(np.uint32))
+    _eq("pidx", from_dev(d_pi), pi)
+    _eq("out", from_dev(d_out), out)
+
+
+def _gpu_route(ctx, ids, T, topk):
+    nblk = (T + 255) // 256
+    cap = T * topk + E * 128
+    d_ids = to_dev(ids)
+    bc = torch.empty(nblk * E, dtype=torch.int32, device="cuda")
+    bo = torch.empty(nblk * E, dtype=torch.int32, device="cuda")
+    cb = torch.full((cap // 128 + 1,), -1, dtype=torch.int32, device="cuda")
+    cl = torch.full((cap // 128 + 1,), -1, dtype=torch.int32, device="cuda")
+    nne = torch.zeros(1, dtype=torch.int32, device="cuda")
+    tp = torch.zeros(1, dtype=torch.int32, device="cuda")
+    rmap = torch.full((cap,), -1, dtype=torch.int32, device="cuda")
+    e2p = torch.empty(T * topk, dtype=torch.int32, device="cuda")
+    ctx.moe_route_count(d_ids, T, RANK, E, bc, topk=topk)
+    ctx.moe_route_tables(bc, nblk, E, 128, bo, cb, cl, nne, tp, rmap)
+    ctx.moe_route_scatter(d_ids, bo, T, RANK, E, rmap, e2p, topk=topk)
+    torch.cuda.synchronize()
+    return dict(bc=bc, bo=bo, cb=cb, cl=cl, nne=nne, tp=tp, rmap=rmap, e2p=e2p)
+
+
+@pytest.mark.parametrize("T,topk", [(16384, 8), (16384, 16), (300, 16), (257, 8)])
+def test_ep_routing_tables(ctx, T, topk):
+    _case(f"routing T={T} topk={topk}")
+    S, bias, rs = _router_inputs(T, 1500 + T + topk)
+    ids, _ = O.router_topk(S, bias, rs[0], T, topk)
+    nblk = (T + 255) // 256
+    bc = O.route_count(ids, T, topk, RANK, E)
+    tab = O.route_tables(bc, nblk, E, 128, T * topk + E * 128)
+    rmap, e2p = O.route_scatter(ids, tab["blockoff"], T, topk, RANK, E, tab["route_map"])
+    d = _gpu_route(ctx, ids, T, topk)
+    _eq("blockcount", from_dev(d["bc"]), bc)
+    _eq("blockoff", from_dev(d["bo"]), tab["blockoff"])
+    nne, tp = tab["num_non_exiting"], tab["total_padded"]
+    assert from_dev(d["nne"])[0] == nne and from_dev(d["tp"])[0] == tp
+    _eq("cta_batch", from_dev(d["cb"])[:nne], tab["cta_batch"][:nne])
+    _eq("cta_limit", from_dev(d["cl"])[:nne], tab["cta_limit"][:nne])
+    _eq("route_map", from_dev(d["rmap"])[:tp], rmap[:tp])
+    _eq("exp2perm", from_dev(d["e2p"]), e2p)
+
+
+def test_permute_and_finalize_config5(ctx):
+    """Config 5: 16384 tokens, top-8 of 224, EP rank 0 of 4 (56 local experts):
+    router -> tables -> MXFP8 permute of the quantised activations -> finalize of
+    bf16 expert outputs over the permuted rows."""
+    T, topk, H = 16384, 8, 7168
+    _case("config5 permute + finalize")
+    S, bias, rs = _router_inputs(T, 1600)
+    ids, wts = O.router_topk(S, bias, rs[0], T, topk)
+    d = _gpu_route(ctx, ids, T, topk)
+    tp = int(from_dev(d["tp"])[0])
+    rmap = from_dev(d["rmap"])[:tp]
+    g = rng(1601)
+    x = normal_bf16(g, (T, H), outlier_p=0.001)
+    q, sf = O.moe_quant(x, T, H)
+    pq = torch.empty((tp, H), dtype=torch.uint8, device="cuda")
+    psf = torch.empty((tp, H // 32), dtype=torch.uint8, device="cuda")
+    ctx.moe_permute_mx(to_dev(q), to_dev(sf), d["rmap"], d["tp"], H, pq, psf)
+    torch.cuda.synchronize()
+    wpq, wpsf = O.moe_permute_mx(q, sf, rmap, tp, H)
+    _eq("pq", from_dev(pq), wpq)
+    _eq("psf", from_dev(psf), wpsf)
+    del pq, psf
+    fc2 = normal_bf16(g, (tp, H))
+    out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    ctx.moe_finalize(to_dev(fc2), d["e2p"], to_dev(wts), out, T, H, topk=topk)
+    torch.cuda.synchronize()
+    want = O.moe_finalize(fc2, from_dev(d["e2p"]), wts, T, topk, H)
+    _eq("finalize", from_dev(out), want)
+
+
+@pytest.mark.parametrize("cols", [3584, 7168, 8])
+def test_finalize_cols(ctx, cols):
+    T, topk = 1000, 16
+    _case(f"finalize cols={cols}")
+    S, bias, rs = _router_inputs(T, 1700 + cols)
+    ids, wts = O.router_topk(S, bias, rs[0], T, topk)
+    d = _gpu_route(ctx, ids, T, topk)
+    tp = int(from_dev(d["tp"])[0])
+    fc2 = normal_bf16(rng(1701), (tp, cols))
+    out = torch.empty((T, cols), dtype=torch.bfloat16, device="cuda")
+    ctx.moe_finalize(to_dev(fc2), d["e2p"], to_dev(wts), out, T, cols, topk=topk)
+    torch.cuda.synchronize()
+    _eq("finalize", from_dev(out), O.moe_finalize(fc2, from_dev(d["e2p"]), wts, T, topk, cols))
+
+
+def test_weight_layouts(ctx):
+    _case("w_shuffle / sf_shuffle")
+    g = rng(1800)
+    experts, n, rb, kg = 3, 256, 64, 8
+    src = g.integers(0, 256, (experts * n * rb,), dtype=np.uint8)
+    s2 = g.integers(0, 256, (experts * n * kg,), dtype=np.uint8)
+    for gated in (0, 1):
+        dst = torch.empty_like(to_dev(src))
+        ctx.moe_w_shuffle(to_dev(src), dst, experts, n, rb, gated)
+        d2 = torch.empty_like(to_dev(s2))
+        ctx.moe_sf_shuffle(to_dev(s2), d2, experts, n, kg, gated)
+        torch.cuda.synchronize()
+        _eq("w_shuffle", from_dev(dst), O.moe_w_shuffle(src, experts, n, rb, gated))
+        _eq("sf_shuffle", from_dev(d2), O.moe_sf_shuffle(s2, experts, n, kg, gated))
+
+
+def test_manifest_router_and_routing_ops(ctx):
+    """ops router_topk, moe_route_count (v3 module), moe_route_tables and
+    moe_route_scatter (v4 module) and moe_finalize (v3) of the default manifest."""
+    ops = json.load(open(os.path.join(GOLDEN, "manifest_hot_ops.json")))
+    tokens = 4096
+    B = tokens // 4  # router rows: ceil(tokens / 4)
+    env = {"tokens": tokens}
+    S, bias, rs = _router_inputs(B, 1900)
+    idx = torch.empty((B, 16), dtype=torch.int32, device="cuda")
+    wts = torch.empty((B, 16), dtype=torch.float32, device="cuda")
+    _case("manifest router_topk")
+    k3h.ManifestOp(ctx, "router_topk", ops["router_topk"])(
+        [to_dev(S), to_dev(bias), to_dev(rs), idx, wts, B], env)
+    torch.cuda.synchronize()
+    wi, ww = O.router_topk(S, bias, rs[0], B, 16)
+    _eq("idx", from_dev(idx), wi)
+    _eq("wts", from_dev(wts).view(np.uint32), ww.view(np.uint32))
+    # routing over all gathered tokens (the manifest routes `tokens` ids rows)
+    S2, b2, _ = _router_inputs(tokens, 1901)
+    ids, w16 = O.router_topk(S2, b2, rs[0], tokens, 16)
+    nblk = tokens // 256
+    cap = tokens * 16 + E * 128
+    bc = torch.empty(nblk * E, dtype=torch.int32, device="cuda")
+    bo = torch.empty_like(bc)
+    cb = torch.empty(cap // 128 + 1, dtype=torch.int32, device="cuda")
+    cl = torch.empty_like(cb)
+    nne = torch.zeros(1, dtype=torch.int32, device="cuda")
+    tp = torch.zeros(1, dtype=torch.int32, device="cuda")
+    rmap = torch.full((cap,), -1, dtype=torch.int32, device="cuda")
+    e2p = torch.empty(tokens * 16, dtype=torch.int32, device="cuda")
+    d_ids = to_dev(ids)
+    _case("manifest moe_route_*")
+    k3h.ManifestOp(ctx, "moe_route_count", ops["moe_route_count"])([d_ids, tokens, RANK, bc], env)
+    k3h.ManifestOp(ctx, "moe_route_tables", ops["moe_route_tables"])(
+        [bc, nblk, bo, cb, cl, nne, tp, rmap], env)
+    k3h.ManifestOp(ctx, "moe_route_scatter", ops["moe_route_scatter"])(
+        [d_ids, bo, tokens, RANK, rmap, e2p], env)
+    torch.cuda.synchronize()
+    obc = O.route_count(ids, tokens, 16, RANK, E)
+    tab = O.route_tables(obc, nblk, E, 128, cap)
+    wr, we = O.route_scatter(ids, tab["blockoff"], tokens, 16, RANK, E, tab["route_map"])
+    t = tab["total_padded"]
+    assert from_dev(tp)[0] == t
+    _eq("route_map", from_dev(rmap)[:t], wr[:t])
+    _eq("exp2perm", from_dev(e2p), we)
+    # finalize at the manifest's cols = 3584
+    _case("manifest moe_finalize")
+    fc2 = normal_bf16(rng(1902), (t, 3584))
+    out = torch.empty((tokens, 3584), dtype=torch.bfloat16, device="cuda")
+    k3h.ManifestOp(ctx, "moe_finalize", ops["moe_finalize"])(
+        [to_dev(fc2), e2p, to_dev(w16), out, tokens], env)
+    torch.cuda.synchronize()
+    _eq("finalize", from_dev(out), O.moe_finalize(fc2, we, w16, tokens, 16, 3584))
