@@ -164,6 +164,23 @@ K3H_API int k3h_moe_w_shuffle(k3h_ctx_t ctx, void* stream, const void* src, void
 K3H_API int k3h_moe_sf_shuffle(k3h_ctx_t ctx, void* stream, const void* src, void* dst,
                                int experts, int n, int kg, int gated);
 
+/* ---- KDA (modules k3_span_gather_v3+HEADS=24, k3_kda_out_gate_v3+HEADS=24) ----
+ * kern_k3_span_gather (k3_span_gather_v3.cu:251; op span_gather_v2, json:406197):
+ * partial bf16 [rows, 4*3072] (q|k|v|g bands), cw f32 [3][4][3072], kda_base:
+ * the KDA state (windows at line_index[at]*line_bytes + 24*128*128*4 + s*18432),
+ * wsm_partial f32 [rows, 256] -> span_q/k/v bf16 [span, 3072], span_beta bf16
+ * [24*span], span_flow bf16 [span, 128].  span_at: device i32 [1]. */
+K3H_API int k3h_span_gather(k3h_ctx_t ctx, void* stream, const void* partial, const float* cw,
+                            void* kda_base, const int* line_index, long long line_bytes,
+                            const float* wsm_partial, void* span_q, void* span_k, void* span_v,
+                            void* span_beta, void* span_flow, const int* span_at, int span);
+/* kern_k3_kda_out_gate (k3_kda_out_gate_v3.cu:36; op kda_out_gate_v2,
+ * json:406169): attn bf16 [span, 3072], gate band 3 of gate_partial bf16
+ * [rows, 12288], gamma_o f32 [128] -> gated bf16 rows [at, at + span). */
+K3H_API int k3h_kda_out_gate(k3h_ctx_t ctx, void* stream, const void* attn,
+                             const void* gate_partial, const float* gamma_o, void* gated,
+                             const int* span_at, int span);
+
 /* ---- measurement support --------------------------------------------------
  * k3h_stream_copy: dst[i] = src[i] for n16 16-byte vectors with non-temporal
  * loads and stores, one vector per thread (module k3h_fused).  No reference

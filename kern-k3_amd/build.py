@@ -38,6 +38,8 @@ SOURCES = {
     "k3_quant_fp8_pair": "k3_quant_fp8_pair.hip",
     "k3_quant_fp8_pair_v2": "k3_quant_fp8_pair.hip",
     "k3_router_argmax": "k3_router_argmax.hip",
+    "k3_span_gather_v3": "k3_span_gather.hip",
+    "k3_kda_out_gate_v3": "k3_kda_out_gate.hip",
 }
 
 # defines implied by a base name that shares its source with another base
@@ -60,6 +62,8 @@ MODULES = [
     "k3_quant_fp8_pair_v2",
     "k3_router_argmax",
     "k3_router_argmax+TOPK=8",
+    "k3_span_gather_v3+HEADS=24",
+    "k3_kda_out_gate_v3+HEADS=24",
 ]
 
 DEVICE_FLAGS = [
@@ -70,7 +74,7 @@ DEVICE_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
-HOST_SOURCES = ["k3h_module.cpp", "k3h_ops_residual.cpp", "k3h_ops_quant.cpp", "k3h_ops_moe.cpp"]
+HOST_SOURCES = ["k3h_module.cpp", "k3h_ops_residual.cpp", "k3h_ops_quant.cpp", "k3h_ops_moe.cpp", "k3h_ops_kda.cpp"]
 
 
 def module_defines(key: str) -> tuple[str, list[str]]:

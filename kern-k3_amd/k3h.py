@@ -78,6 +78,8 @@ _SIGS: dict[str, list] = {
     "k3h_moe_permute_mx": [_P, _P, _P, _P, _P, _P, _I, _P, _P],
     "k3h_moe_w_shuffle": [_P, _P, _P, _P, _I, _I, _I, _I],
     "k3h_moe_sf_shuffle": [_P, _P, _P, _P, _I, _I, _I, _I],
+    "k3h_span_gather": [_P, _P, _P, _P, _P, _P, ctypes.c_int64, _P, _P, _P, _P, _P, _P, _P, _I],
+    "k3h_kda_out_gate": [_P, _P, _P, _P, _P, _P, _P, _I],
 }
 
 
@@ -356,6 +358,38 @@ class Ctx:
         _dev(dst, "dst", U8, experts * n * kg, align=1)
         _check(self.L.k3h_moe_sf_shuffle(self.h, _stream(stream), _ptr(src), _ptr(dst), experts, n,
                                          kg, gated), "moe_sf_shuffle")
+
+    # ------------------------------------------------------------ KDA
+    def span_gather(self, partial, cw, kda_base, line_index, line_bytes: int, wsm_partial, span_q,
+                    span_k, span_v, span_beta, span_flow, span_at, span: int, stream=None) -> None:
+        """Manifest op span_gather_v2 -- kern_k3_span_gather, HEADS = 24."""
+        inner = 3072
+        _dev(partial, "partial", BF16, 4 * inner)
+        _dev(cw, "cw", F32, 12 * inner)
+        _dev(kda_base, "kda_base", (kda_base.dtype,))
+        _dev(line_index, "line_index", I32, 1, align=4)
+        _dev(wsm_partial, "wsm_partial", F32, 256)
+        for nm, t in (("span_q", span_q), ("span_k", span_k), ("span_v", span_v)):
+            _dev(t, nm, BF16, span * inner)
+        _dev(span_beta, "span_beta", BF16, 24 * span, align=2)
+        _dev(span_flow, "span_flow", BF16, span * 128)
+        _dev(span_at, "span_at", I32, 1, align=4)
+        _check(self.L.k3h_span_gather(self.h, _stream(stream), _ptr(partial), _ptr(cw), _ptr(kda_base),
+                                      _ptr(line_index), line_bytes, _ptr(wsm_partial), _ptr(span_q),
+                                      _ptr(span_k), _ptr(span_v), _ptr(span_beta), _ptr(span_flow),
+                                      _ptr(span_at), span), "span_gather")
+
+    def kda_out_gate(self, attn, gate_partial, gamma_o, gated, span_at, span: int,
+                     stream=None) -> None:
+        """Manifest op kda_out_gate_v2 -- kern_k3_kda_out_gate, HEADS = 24."""
+        _dev(attn, "attn", BF16, span * 3072)
+        _dev(gate_partial, "gate_partial", BF16, 4 * 3072)
+        _dev(gamma_o, "gamma_o", F32, 128)
+        _dev(gated, "gated", BF16, 3072)
+        _dev(span_at, "span_at", I32, 1, align=4)
+        _check(self.L.k3h_kda_out_gate(self.h, _stream(stream), _ptr(attn), _ptr(gate_partial),
+                                       _ptr(gamma_o), _ptr(gated), _ptr(span_at), span),
+               "kda_out_gate")
 
     # ------------------------------------------------------------ measurement
     def stream_copy(self, src, dst, stream=None) -> None:

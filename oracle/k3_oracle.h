@@ -90,6 +90,13 @@ void k3o_moe_w_shuffle(const uint8_t* src, uint8_t* dst, int experts, int n, int
                        int gated);
 void k3o_moe_sf_shuffle(const uint8_t* src, uint8_t* dst, int experts, int n, int kg, int gated);
 
+/* ---- KDA span gather / output gate (k3_span_gather_v3.cu, k3_kda_out_gate_v3.cu) */
+void k3o_span_gather(const uint16_t* partial, const float* cw, uint16_t* win, const float* wsm,
+                     uint16_t* span_q, uint16_t* span_k, uint16_t* span_v, uint16_t* span_beta,
+                     uint16_t* span_flow, int at, int span, int heads);
+void k3o_kda_out_gate(const uint16_t* attn, const uint16_t* gate_partial, const float* gamma_o,
+                      uint16_t* gated, int at, int span, int heads);
+
 int k3o_num_threads(void);
 
 #ifdef __cplusplus

@@ -240,3 +240,26 @@ def moe_sf_shuffle(src, experts, n, kg, gated):
     dst = np.empty_like(src)
     lib().k3o_moe_sf_shuffle(_p(src), _p(dst), experts, n, kg, gated)
     return dst
+
+
+# ---------------------------------------------------------------- KDA
+def span_gather(partial, cw, win, wsm, at, span, heads=24):
+    """Returns (q, k, v, beta, flow, new_win); win [3, 3, inner] bf16 is not modified."""
+    inner = heads * 128
+    w = np.ascontiguousarray(win, np.uint16).copy()
+    q = np.empty((span, inner), np.uint16)
+    k = np.empty((span, inner), np.uint16)
+    v = np.empty((span, inner), np.uint16)
+    beta = np.empty(heads * span, np.uint16)
+    flow = np.empty((span, 128), np.uint16)
+    lib().k3o_span_gather(_p(np.ascontiguousarray(partial)), _p(np.ascontiguousarray(cw, np.float32)),
+                          _p(w), _p(np.ascontiguousarray(wsm, np.float32)), _p(q), _p(k), _p(v),
+                          _p(beta), _p(flow), at, span, heads)
+    return q, k, v, beta, flow, w
+
+
+def kda_out_gate(attn, gate_partial, gamma_o, gated_in, at, span, heads=24):
+    gated = np.ascontiguousarray(gated_in, np.uint16).copy()
+    lib().k3o_kda_out_gate(_p(np.ascontiguousarray(attn)), _p(np.ascontiguousarray(gate_partial)),
+                           _p(np.ascontiguousarray(gamma_o, np.float32)), _p(gated), at, span, heads)
+    return gated

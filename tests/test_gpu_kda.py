@@ -1,0 +1,147 @@
+"""GPU parity: KDA span gather (conv + SiLU, beta/flow landing, window update)
+and output gate (per-head RMS x gamma_o x sigmoid gate) against the C oracle.
+Bar: landing copies and the window bit-exact; conv/SiLU and gate outputs within
+one bf16 ulp (the kernels use the hardware 2^x / reciprocal logistic, the
+checker the exact one), with the differing fraction reported and bounded."""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import k3h
+import oracle as O
+from k3data import bf16_to_f32, from_dev, normal_bf16, rng, to_dev, ulp_diff_bf16
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+HEADS, INNER = 24, 3072
+LINE_BYTES = 1628160
+REC_BYTES = HEADS * 128 * 128 * 4
+WIN_BYTES = 3 * INNER * 2
+
+
+def _case(m):
+    print(f"[case] {m}", flush=True)
+
+
+def _close1(name, got, want, frac=2e-3):
+    d = ulp_diff_bf16(np.asarray(got), np.asarray(want))
+    print(f"  {name}: max ulp {d.max()}, differing {(d > 0).mean():.2e}", flush=True)
+    assert d.max() <= 1 and (d > 0).mean() < frac, name
+
+
+class Span:
+    """Device buffers of one span_gather call over `rows` batch rows; the KDA
+    state holds 3 lines and the span's windows live in line `line`."""
+
+    def __init__(self, rows, seed, line=1):
+        g = rng(seed)
+        self.partial = normal_bf16(g, (rows, 4 * INNER))
+        self.cw = bf16_to_f32(normal_bf16(g, (3, 4, INNER), 0.0, 0.5))
+        self.win = normal_bf16(g, (3, 3, INNER))
+        self.wsm = g.standard_normal((rows, 256), dtype=np.float32)
+        self.line = line
+        state = g.integers(0, 256, 3 * LINE_BYTES, dtype=np.uint8)
+        off = line * LINE_BYTES + REC_BYTES
+        state[off:off + 3 * WIN_BYTES] = self.win.reshape(-1).view(np.uint8)
+        self.state0 = state
+        self.d_state = to_dev(state)
+        self.d_partial, self.d_cw, self.d_wsm = to_dev(self.partial), to_dev(self.cw), to_dev(self.wsm)
+        self.d_line = to_dev(np.full(rows, line, np.int32))
+
+    def window(self):
+        st = from_dev(self.d_state)
+        off = self.line * LINE_BYTES + REC_BYTES
+        return st[off:off + 3 * WIN_BYTES].view(np.uint16).reshape(3, 3, INNER), st
+
+    def run(self, ctx, at, span):
+        outs = [torch.empty((span, INNER), dtype=torch.bfloat16, device="cuda") for _ in range(3)]
+        beta = torch.empty(HEADS * span, dtype=torch.bfloat16, device="cuda")
+        flow = torch.empty((span, 128), dtype=torch.bfloat16, device="cuda")
+        ctx.span_gather(self.d_partial, self.d_cw, self.d_state, self.d_line, LINE_BYTES, self.d_wsm,
+                        *outs, beta, flow, to_dev(np.array([at], np.int32)), span)
+        torch.cuda.synchronize()
+        return [from_dev(o) for o in outs] + [from_dev(beta), from_dev(flow)]
+
+
+@pytest.mark.parametrize("rows,at,span", [(16384, 0, 16384), (100, 7, 45), (10, 4, 2), (40, 0, 17)])
+def test_span_gather(ctx, rows, at, span):
+    _case(f"span_gather rows={rows} at={at} span={span}")
+    sp = Span(rows, 2000 + span)
+    q, k, v, beta, flow, nw = O.span_gather(sp.partial, sp.cw, sp.win, sp.wsm, at, span)
+    got = sp.run(ctx, at, span)
+    for nm, gq, wq in zip("qkv", got[:3], (q, k, v)):
+        _close1(f"span_{nm}", gq, wq)
+    assert np.array_equal(got[3], beta) and np.array_equal(got[4], flow)
+    win, st = sp.window()
+    assert np.array_equal(win, nw)
+    off = sp.line * LINE_BYTES + REC_BYTES
+    rest = np.ones(st.size, bool)
+    rest[off:off + 3 * WIN_BYTES] = False
+    assert np.array_equal(st[rest], sp.state0[rest]), "span_gather wrote outside the window"
+
+
+def test_span_gather_split_spans_match_one_span(ctx):
+    """Window protocol on the GPU: spans 16 + 1 + 23 continue exactly as one span of 40."""
+    _case("span_gather split spans")
+    a = Span(48, 2100)
+    one = a.run(ctx, 3, 40)
+    w_one, _ = a.window()
+    b = Span(48, 2100)
+    parts, at = [], 3
+    for n in (16, 1, 23):
+        parts.append(b.run(ctx, at, n))
+        at += n
+    w_split, _ = b.window()
+    for j in range(3):
+        assert np.array_equal(np.concatenate([p[j] for p in parts]), one[j])
+    assert np.array_equal(w_split, w_one)
+
+
+@pytest.mark.parametrize("rows,at,span", [(16384, 0, 16384), (50, 9, 33)])
+def test_kda_out_gate(ctx, rows, at, span):
+    _case(f"kda_out_gate rows={rows} at={at} span={span}")
+    g = rng(2200 + span)
+    attn = normal_bf16(g, (span, INNER))
+    gate = normal_bf16(g, (rows, 4 * INNER))
+    gamma_o = (1.0 + 0.1 * g.standard_normal(128)).astype(np.float32)
+    want = O.kda_out_gate(attn, gate, gamma_o, np.zeros((rows, INNER), np.uint16), at, span)
+    gated = torch.zeros((rows, INNER), dtype=torch.bfloat16, device="cuda")
+    ctx.kda_out_gate(to_dev(attn), to_dev(gate), to_dev(gamma_o), gated,
+                     to_dev(np.array([at], np.int32)), span)
+    torch.cuda.synchronize()
+    got = from_dev(gated)
+    _close1("gated", got[at:at + span], want[at:at + span])
+    assert not got[:at].any() and not got[at + span:].any()
+
+
+def test_manifest_kda_ops(ctx):
+    ops = json.load(open(os.path.join(GOLDEN, "manifest_hot_ops.json")))
+    tokens = 64
+    env = {"tokens": tokens}
+    _case("manifest span_gather_v2")
+    sp = Span(tokens, 2300)
+    outs = [torch.empty((tokens, INNER), dtype=torch.bfloat16, device="cuda") for _ in range(3)]
+    beta = torch.empty(HEADS * tokens, dtype=torch.bfloat16, device="cuda")
+    flow = torch.empty((tokens, 128), dtype=torch.bfloat16, device="cuda")
+    at_d = to_dev(np.array([0], np.int32))
+    k3h.ManifestOp(ctx, "span_gather_v2", ops["span_gather_v2"])(
+        [sp.d_partial, sp.d_cw, sp.d_state, sp.d_line, sp.d_wsm, *outs, beta, flow, at_d, tokens], env)
+    torch.cuda.synchronize()
+    q, k, v, wb, wf, nw = O.span_gather(sp.partial, sp.cw, sp.win, sp.wsm, 0, tokens)
+    for nm, o, w in zip("qkv", outs, (q, k, v)):
+        _close1(f"span_{nm}", from_dev(o), w)
+    assert np.array_equal(from_dev(beta), wb) and np.array_equal(from_dev(flow), wf)
+    assert np.array_equal(sp.window()[0], nw)
+    _case("manifest kda_out_gate_v2")
+    g = rng(2301)
+    attn = normal_bf16(g, (tokens, INNER))
+    gamma_o = (1.0 + 0.1 * g.standard_normal(128)).astype(np.float32)
+    gated = torch.zeros((tokens, INNER), dtype=torch.bfloat16, device="cuda")
+    k3h.ManifestOp(ctx, "kda_out_gate_v2", ops["kda_out_gate_v2"])(
+        [to_dev(attn), sp.d_partial, to_dev(gamma_o), gated, at_d, tokens], env)
+    torch.cuda.synchronize()
+    want = O.kda_out_gate(attn, sp.partial, gamma_o, np.zeros((tokens, INNER), np.uint16), 0, tokens)
+    _close1("gated", from_dev(gated), want)
