@@ -181,6 +181,28 @@ K3H_API int k3h_kda_out_gate(k3h_ctx_t ctx, void* stream, const void* attn,
                              const void* gate_partial, const float* gamma_o, void* gated,
                              const int* span_at, int span);
 
+/* ---- MLA --------------------------------------------------------------------
+ * kern_k3_mla_prep_head + kern_k3_mla_prep_gate (k3_mla_prep_v2.cu:91,130;
+ * k3_mla_prep_bf16.cu:73,112; manifest op mla_prep, json:404677): partial
+ * [B, 5184] f32 (bf16_partial = 0, module k3_mla_prep_v2+...) or bf16
+ * (module k3_mla_prep_bf16+...); gammas bf16; slot_mapping i64 [B]; slab bf16
+ * paged latent (element offsets layer_off, page_stride; 884736 in the manifest)
+ * -> q_norm bf16 [B, 1536], latent rows in the slab, mla_gate bf16 [B, 3072]. */
+K3H_API int k3h_mla_prep(k3h_ctx_t ctx, void* stream, int bf16_partial, const void* partial,
+                         const void* gamma_q_a, const void* gamma_kv_a,
+                         const long long* slot_mapping, void* slab, long long layer_off,
+                         long long page_stride, void* q_norm, void* mla_gate, int B);
+/* k3h_mla_rope_pack: no reference entry (the reference has no RoPE on this
+ * path; its rope columns are a bf16 landing, k3_mla_prep_v2.cu:205-210).
+ * latent bf16 [T,512], k_rope bf16 [T,64], q bf16 [T,H,192], gamma_kv bf16
+ * [512], positions i64 [T] -> latent_out bf16 [T,576] = RMSNorm(latent) |
+ * rope(k_rope), q_out bf16 [T,H,192] = nope | rope(q_rope); interleaved pairs,
+ * angle p * theta^(-2j/64). */
+K3H_API int k3h_mla_rope_pack(k3h_ctx_t ctx, void* stream, const void* latent,
+                              const void* k_rope, const void* q, const void* gamma_kv,
+                              const long long* positions, void* latent_out, void* q_out,
+                              float theta, float eps, int T, int H);
+
 /* ---- measurement support --------------------------------------------------
  * k3h_stream_copy: dst[i] = src[i] for n16 16-byte vectors with non-temporal
  * loads and stores, one vector per thread (module k3h_fused).  No reference

@@ -40,11 +40,15 @@ SOURCES = {
     "k3_router_argmax": "k3_router_argmax.hip",
     "k3_span_gather_v3": "k3_span_gather.hip",
     "k3_kda_out_gate_v3": "k3_kda_out_gate.hip",
+    "k3_mla_prep_v2": "k3_mla_prep.hip",
+    "k3_mla_prep_bf16": "k3_mla_prep.hip",
+    "k3h_mla_rope": "k3h_mla_rope.hip",
 }
 
 # defines implied by a base name that shares its source with another base
 IMPLIED = {
     "k3_quant_fp8_pair_v2": ["-DK3_QUANT_V2=1"],
+    "k3_mla_prep_bf16": ["-DK3_MLA_BF16=1"],
 }
 
 # Every module key the host library or the manifests may load.
@@ -64,6 +68,9 @@ MODULES = [
     "k3_router_argmax+TOPK=8",
     "k3_span_gather_v3+HEADS=24",
     "k3_kda_out_gate_v3+HEADS=24",
+    "k3_mla_prep_v2+INNER=3072+MLA_FUSED=5184",
+    "k3_mla_prep_bf16+INNER=3072+MLA_FUSED=5184",
+    "k3h_mla_rope",
 ]
 
 DEVICE_FLAGS = [
@@ -74,7 +81,7 @@ DEVICE_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
-HOST_SOURCES = ["k3h_module.cpp", "k3h_ops_residual.cpp", "k3h_ops_quant.cpp", "k3h_ops_moe.cpp", "k3h_ops_kda.cpp"]
+HOST_SOURCES = ["k3h_module.cpp", "k3h_ops_residual.cpp", "k3h_ops_quant.cpp", "k3h_ops_moe.cpp", "k3h_ops_kda.cpp", "k3h_ops_mla.cpp"]
 
 
 def module_defines(key: str) -> tuple[str, list[str]]:

@@ -80,6 +80,8 @@ _SIGS: dict[str, list] = {
     "k3h_moe_sf_shuffle": [_P, _P, _P, _P, _I, _I, _I, _I],
     "k3h_span_gather": [_P, _P, _P, _P, _P, _P, ctypes.c_int64, _P, _P, _P, _P, _P, _P, _P, _I],
     "k3h_kda_out_gate": [_P, _P, _P, _P, _P, _P, _P, _I],
+    "k3h_mla_prep": [_P, _P, _I, _P, _P, _P, _P, _P, ctypes.c_int64, ctypes.c_int64, _P, _P, _I],
+    "k3h_mla_rope_pack": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _F, _I, _I],
 }
 
 
@@ -390,6 +392,36 @@ class Ctx:
         _check(self.L.k3h_kda_out_gate(self.h, _stream(stream), _ptr(attn), _ptr(gate_partial),
                                        _ptr(gamma_o), _ptr(gated), _ptr(span_at), span),
                "kda_out_gate")
+
+    # ------------------------------------------------------------ MLA
+    def mla_prep(self, partial, gamma_q_a, gamma_kv_a, slot_mapping, slab, layer_off: int,
+                 q_norm, mla_gate, B: int, page_stride: int = 884736, stream=None) -> None:
+        """Manifest op mla_prep (partial, gamma_q_a, gamma_kv_a, slot_mapping, state kv,
+        layer_off, q_norm, mla_gate, B): head launch then gate launch."""
+        _dev(partial, "partial", BF16 + F32, B * 5184)
+        _dev(gamma_q_a, "gamma_q_a", BF16, 1536, align=8)
+        _dev(gamma_kv_a, "gamma_kv_a", BF16, 512, align=8)
+        _dev(slot_mapping, "slot_mapping", I64, B, align=8)
+        _dev(slab, "slab", BF16, 1, align=8)
+        _dev(q_norm, "q_norm", BF16, B * 1536, align=8)
+        _dev(mla_gate, "mla_gate", BF16, B * 3072)
+        _check(self.L.k3h_mla_prep(self.h, _stream(stream), int(partial.dtype == torch.bfloat16),
+                                   _ptr(partial), _ptr(gamma_q_a), _ptr(gamma_kv_a),
+                                   _ptr(slot_mapping), _ptr(slab), layer_off, page_stride,
+                                   _ptr(q_norm), _ptr(mla_gate), B), "mla_prep")
+
+    def mla_rope_pack(self, latent, k_rope, q, gamma_kv, positions, latent_out, q_out, T: int,
+                      H: int, theta: float = 50000.0, eps: float = 1e-6, stream=None) -> None:
+        _dev(latent, "latent", BF16, T * 512)
+        _dev(k_rope, "k_rope", BF16, T * 64)
+        _dev(q, "q", BF16, T * H * 192)
+        _dev(gamma_kv, "gamma_kv", BF16, 512)
+        _dev(positions, "positions", I64, T, align=8)
+        _dev(latent_out, "latent_out", BF16, T * 576)
+        _dev(q_out, "q_out", BF16, T * H * 192)
+        _check(self.L.k3h_mla_rope_pack(self.h, _stream(stream), _ptr(latent), _ptr(k_rope), _ptr(q),
+                                        _ptr(gamma_kv), _ptr(positions), _ptr(latent_out),
+                                        _ptr(q_out), theta, eps, T, H), "mla_rope_pack")
 
     # ------------------------------------------------------------ measurement
     def stream_copy(self, src, dst, stream=None) -> None:

@@ -97,6 +97,15 @@ void k3o_span_gather(const uint16_t* partial, const float* cw, uint16_t* win, co
 void k3o_kda_out_gate(const uint16_t* attn, const uint16_t* gate_partial, const float* gamma_o,
                       uint16_t* gated, int at, int span, int heads);
 
+/* ---- MLA (k3_mla_prep_v2.cu / k3_mla_prep_bf16.cu; RoPE + pack) -------------- */
+void k3o_mla_prep(const float* partial_f32, const uint16_t* partial_bf16, int mla_fused,
+                  int inner, const uint16_t* gamma_q_a, const uint16_t* gamma_kv_a,
+                  const long long* slot_mapping, uint16_t* slab, long long layer_off,
+                  long long page_stride, uint16_t* q_norm, uint16_t* mla_gate, int B);
+void k3o_mla_rope_pack(const uint16_t* latent, const uint16_t* k_rope, const uint16_t* q,
+                       const uint16_t* gamma_kv, const long long* positions, uint16_t* latent_out,
+                       uint16_t* q_out, float theta, float eps, int T, int H);
+
 int k3o_num_threads(void);
 
 #ifdef __cplusplus

@@ -263,3 +263,29 @@ def kda_out_gate(attn, gate_partial, gamma_o, gated_in, at, span, heads=24):
     lib().k3o_kda_out_gate(_p(np.ascontiguousarray(attn)), _p(np.ascontiguousarray(gate_partial)),
                            _p(np.ascontiguousarray(gamma_o, np.float32)), _p(gated), at, span, heads)
     return gated
+
+
+# ---------------------------------------------------------------- MLA
+def mla_prep(partial, gamma_q_a, gamma_kv_a, slot_mapping, slab_in, layer_off, page_stride, B,
+             inner=3072, mla_fused=5184):
+    """Returns (slab, q_norm, mla_gate); partial float32 or uint16 (bf16) [B, mla_fused]."""
+    slab = np.ascontiguousarray(slab_in, np.uint16).copy()
+    q_norm = np.empty((B, 1536), np.uint16)
+    gate = np.empty((B, inner), np.uint16)
+    bf = partial.dtype == np.uint16
+    partial = np.ascontiguousarray(partial)
+    lib().k3o_mla_prep(None if bf else _p(partial), _p(partial) if bf else None, mla_fused, inner,
+                       _p(gamma_q_a), _p(gamma_kv_a), _p(np.ascontiguousarray(slot_mapping, np.int64)),
+                       _p(slab), ctypes.c_longlong(layer_off), ctypes.c_longlong(page_stride),
+                       _p(q_norm), _p(gate), B)
+    return slab, q_norm, gate
+
+
+def mla_rope_pack(latent, k_rope, q, gamma_kv, positions, T, H, theta=50000.0, eps=1e-6):
+    lat = np.empty((T, 576), np.uint16)
+    qo = np.empty((T, H, 192), np.uint16)
+    lib().k3o_mla_rope_pack(_p(np.ascontiguousarray(latent)), _p(np.ascontiguousarray(k_rope)),
+                            _p(np.ascontiguousarray(q)), _p(gamma_kv),
+                            _p(np.ascontiguousarray(positions, np.int64)), _p(lat), _p(qo),
+                            ctypes.c_float(theta), ctypes.c_float(eps), T, H)
+    return lat, qo
