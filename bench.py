@@ -110,6 +110,158 @@ def copy_ceiling(ctx, rows: int, reps: int) -> float:
     return gbs
 
 
+def bench_ops(ctx, reps: int, out_path: str | None) -> list:
+    """Every op at its BASELINE config shape: per-launch HIP events with a 512 MB
+    cache-flush write between launches (outside the events); median of `reps`."""
+    import torch
+    s = torch.cuda.current_stream()
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(24301)
+
+    def bf(*shape, mean=0.0, std=1.0):
+        return (torch.randn(shape, generator=g, device="cuda") * std + mean).to(torch.bfloat16)
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        ts = []
+        for _ in range(reps):
+            flush.fill_(1)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            fn()
+            e1.record(s)
+            e1.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e3)
+        ts.sort()
+        return ts[len(ts) // 2]
+
+    rows = []
+
+    def add(op, kernel, shape, nbytes, us, note=""):
+        gbs = nbytes / (us * 1e-6) / 1e9
+        rows.append({"op": op, "kernel": kernel, "shape": shape, "bytes": int(nbytes),
+                     "us": round(us, 2), "gbs": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1),
+                     "note": note})
+        log(f"{op:34s} {us:9.2f} us {gbs:8.0f} GB/s {100 * gbs / PEAK_GBS:5.1f}%  {note}")
+
+    T = 16384
+    # copy ceiling
+    a = torch.empty(T * H, dtype=torch.bfloat16, device="cuda").fill_(1)
+    b = torch.empty_like(a)
+    add("stream copy (ceiling)", "k3h_stream_copy", f"{T}x{H} bf16", 4 * T * H,
+        timed(lambda: ctx.stream_copy(a, b, stream=s)))
+    del a, b
+    # config 1: K1b nb = 0 at 1024 x 7168, eps 1e-6
+    B1 = 1024
+    p1, r1, g1 = bf(B1, H), bf(B1, H), bf(H, mean=1.0, std=0.1)
+    o1, n1 = torch.empty_like(p1), torch.empty_like(p1)
+    sw = torch.zeros(H, dtype=torch.float32, device="cuda")
+    add("residual add + RMSNorm (cfg 1)", "kern_k3_land_add_attnres_rms", f"{B1}x{H}",
+        4 * B1 * H * 2 + H * 2,
+        timed(lambda: ctx.land_add_attnres_rms(p1, r1, None, sw, g1, o1, n1, 0, 0, B1, eps=1e-6, stream=s)))
+    # config 2: fused, and the standalone quantisers at the same shape
+    x, res, gm = make_inputs(T)
+    ro = torch.empty_like(x)
+    q = torch.empty((T, H), dtype=torch.uint8, device="cuda")
+    sf = torch.empty((T, H // 32), dtype=torch.uint8, device="cuda")
+    add("residual+RMSNorm+MXFP8 (cfg 2)", "k3h_residual_rms_mxfp8", f"{T}x{H}", algo_bytes(T),
+        timed(lambda: ctx.residual_rms_mxfp8(x, res, gm, ro, q, sf, None, eps=1e-6, B=T, stream=s)))
+    add("MXFP8 quant alone", "kern_k3_moe_quant", f"{T}x{H}", T * H * 2 + T * H + T * H // 32,
+        timed(lambda: ctx.moe_quant(x, q, sf, T, H, stream=s)))
+    sc = torch.empty(1, dtype=torch.float32, device="cuda")
+    parts = torch.empty(2048, dtype=torch.float32, device="cuda")
+    add("per-tensor fp8 pair (amax+apply)", "kern_quant_fp8_{amax,apply}_v2", f"{T}x{H}",
+        2 * T * H * 2 + T * H, timed(lambda: ctx.quant_fp8_tensor(x, q, sc, parts, T * H, stream=s)))
+    del ro, q, sf
+    # config 3: KDA span gather + output gate (24 heads x 128)
+    inner = 3072
+    part = bf(T, 4 * inner)
+    cw = (torch.randn((3, 4, inner), generator=g, device="cuda") * 0.5).to(torch.bfloat16).float()
+    state = torch.zeros(2 * 1628160, dtype=torch.uint8, device="cuda")
+    line = torch.zeros(T, dtype=torch.int32, device="cuda")
+    wsm = torch.randn((T, 256), generator=g, device="cuda")
+    sq, sk, sv = (torch.empty((T, inner), dtype=torch.bfloat16, device="cuda") for _ in range(3))
+    beta = torch.empty(24 * T, dtype=torch.bfloat16, device="cuda")
+    flow = torch.empty((T, 128), dtype=torch.bfloat16, device="cuda")
+    at0 = torch.zeros(1, dtype=torch.int32, device="cuda")
+    add("KDA span gather (cfg 3a)", "kern_k3_span_gather", f"T={T} 24x128",
+        3 * T * inner * 2 * 2 + 3 * 4 * inner * 4 + 2 * 3 * 3 * inner * 2 + T * (24 + 128) * 4 + T * 24 * 2 + T * 128 * 2,
+        timed(lambda: ctx.span_gather(part, cw, state, line, 1628160, wsm, sq, sk, sv, beta, flow, at0, T, stream=s)))
+    attn = bf(T, inner)
+    gam = torch.ones(128, dtype=torch.float32, device="cuda")
+    gated = torch.empty((T, inner), dtype=torch.bfloat16, device="cuda")
+    add("KDA output gate (cfg 3b)", "kern_k3_kda_out_gate", f"T={T} 24x128",
+        3 * T * inner * 2 + 512, timed(lambda: ctx.kda_out_gate(attn, part, gam, gated, at0, T, stream=s)))
+    del part, sq, sk, sv, attn, gated, wsm
+    # config 4: MLA prep (reference form, bf16 partial) and the RoPE + pack form
+    mp = bf(T, 5184)
+    gq, gk = bf(1536, mean=1.0, std=0.1), bf(512, mean=1.0, std=0.1)
+    slots = torch.arange(T, dtype=torch.int64, device="cuda")
+    slab = torch.empty((T // 64) * 64 * 576, dtype=torch.bfloat16, device="cuda")
+    qn = torch.empty((T, 1536), dtype=torch.bfloat16, device="cuda")
+    mg = torch.empty((T, 3072), dtype=torch.bfloat16, device="cuda")
+    add("MLA prep (cfg 4, reference form)", "kern_k3_mla_prep_{head,gate}", f"T={T} [T,5184] bf16",
+        T * 5184 * 2 + T * (1536 + 576 + 3072) * 2 + 4096,
+        timed(lambda: ctx.mla_prep(mp, gq, gk, slots, slab, 0, qn, mg, T, page_stride=64 * 576, stream=s)))
+    del mp, qn, mg
+    lat, kr, qq = bf(T, 512), bf(T, 64), bf(T, 16, 192)
+    lo = torch.empty((T, 576), dtype=torch.bfloat16, device="cuda")
+    qo = torch.empty_like(qq)
+    add("MLA latent norm + RoPE + q pack", "k3h_mla_rope_pack", f"T={T} H=16",
+        T * (512 + 64 + 16 * 192) * 2 + T * (576 + 16 * 192) * 2,
+        timed(lambda: ctx.mla_rope_pack(lat, kr, qq, gk, slots, lo, qo, T, 16, stream=s)))
+    del lat, kr, qq, lo, qo, slab
+    # config 5: MoE routing + EP dispatch / finalize (top-8 of 224, EP rank 0 of 4)
+    Sx = torch.randn((T, 224), generator=g, device="cuda")
+    bias = torch.randn(224, generator=g, device="cuda") * 0.01
+    rs = torch.full((1,), 2.5, dtype=torch.bfloat16, device="cuda")
+    idx = torch.empty((T, 8), dtype=torch.int32, device="cuda")
+    wts = torch.empty((T, 8), dtype=torch.float32, device="cuda")
+    add("router top-8 (cfg 5a)", "kern_k3_router_topk", f"[{T},224]", T * 224 * 4 + 896 + 2 * T * 8 * 4,
+        timed(lambda: ctx.router_topk(Sx, bias, rs, idx, wts, T, topk=8, stream=s)),
+        "latency-bound (sequential picks)")
+    E, nblk = 56, T // 256
+    cap = T * 8 + E * 128
+    bc = torch.empty(nblk * E, dtype=torch.int32, device="cuda")
+    bo = torch.empty_like(bc)
+    cb = torch.empty(cap // 128 + 1, dtype=torch.int32, device="cuda")
+    cl = torch.empty_like(cb)
+    nne = torch.zeros(1, dtype=torch.int32, device="cuda")
+    tp = torch.zeros(1, dtype=torch.int32, device="cuda")
+    rmap = torch.zeros(cap, dtype=torch.int32, device="cuda")
+    e2p = torch.empty(T * 8, dtype=torch.int32, device="cuda")
+
+    def route():
+        ctx.moe_route_count(idx, T, 0, E, bc, topk=8, stream=s)
+        ctx.moe_route_tables(bc, nblk, E, 128, bo, cb, cl, nne, tp, rmap, stream=s)
+        ctx.moe_route_scatter(idx, bo, T, 0, E, rmap, e2p, topk=8, stream=s)
+    us_route = timed(route)
+    torch.cuda.synchronize()
+    tpad = int(tp.item())
+    live = int((e2p >= 0).sum().item())
+    add("EP routing tables (count+tables+scatter)", "kern_k3_moe_route_{count,tables,scatter}",
+        f"T={T} top-8 E=56", 2 * T * 8 * 4 + 3 * nblk * E * 4 + tpad * 4, us_route,
+        "latency-bound (three launches, one single-workgroup scan)")
+    x8 = torch.randint(0, 256, (T, H), dtype=torch.uint8, device="cuda", generator=g)
+    sf8 = torch.randint(0, 256, (T, H // 32), dtype=torch.uint8, device="cuda", generator=g)
+    pq = torch.empty((tpad, H), dtype=torch.uint8, device="cuda")
+    psf = torch.empty((tpad, H // 32), dtype=torch.uint8, device="cuda")
+    add("MXFP8 permute (cfg 5c)", "k3h_moe_permute_mx", f"{tpad} rows x {H}", 2 * tpad * (H + H // 32),
+        timed(lambda: ctx.moe_permute_mx(x8, sf8, rmap, tp, H, pq, psf, stream=s)))
+    del pq, psf, x8, sf8
+    fc2 = bf(tpad, H)
+    out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    add("weighted finalize (cfg 5d)", "kern_k3_moe_finalize", f"T={T} cols={H}",
+        live * H * 2 + 2 * T * 8 * 4 + T * H * 2,
+        timed(lambda: ctx.moe_finalize(fc2, e2p, wts, out, T, H, topk=8, stream=s)))
+    if out_path:
+        with open(out_path, "w") as f:
+            json.dump(rows, f, indent=1)
+    return rows
+
+
 def load_traffic(kernel: str, workload: str):
     p = os.path.join(REPO, "profiles", "traffic.json")
     try:
@@ -129,6 +281,10 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--op", choices=["fused", "copy"], default="fused",
                     help="copy: only the 16-byte streaming copy (counter calibration)")
+    ap.add_argument("--ops", action="store_true",
+                    help="also time every op at its config shape (table on stderr)")
+    ap.add_argument("--ops-only", action="store_true", help="only the per-op table")
+    ap.add_argument("--ops-out", default=None, help="write the per-op table as JSON")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only (asked for {a.gpus}); the op family shards "
@@ -140,6 +296,9 @@ def main() -> int:
 
     ctx = k3h.Ctx()
     rows = a.rows
+    if a.ops_only:
+        bench_ops(ctx, max(5, min(a.steps, 30)), a.ops_out)
+        return 0
     copy_gbs = copy_ceiling(ctx, rows, a.steps if a.op == "copy" else 20)
     if a.op == "copy":
         print(json.dumps({"op": "k3h_stream_copy", "bytes_per_launch": 2 * rows * H * 2,
@@ -174,6 +333,9 @@ def main() -> int:
             "frac": round(gbs / PEAK_GBS, 4), "traffic": traffic,
             "kernel": "k3h_residual_rms_mxfp8", "algorithmic_bytes": nbytes,
             "avg_launch_us": round(ms * 1e3, 2), "copy_ceiling_gbs": round(copy_gbs, 1)}
+    ops = None
+    if a.ops:
+        ops = bench_ops(ctx, 20, a.ops_out)
     cpu = None
     if not a.no_cpu:
         log("CPU baseline: C oracle on the same inputs")
@@ -190,6 +352,8 @@ def main() -> int:
         "pct_of_peak": round(100 * gbs / PEAK_GBS, 2),
         "roofline": roof, "cpu_baseline": cpu,
     }
+    if ops:
+        line["ops"] = {r["op"]: {"us": r["us"], "gbs": r["gbs"], "pct_peak": r["pct_peak"]} for r in ops}
     print(json.dumps(line), flush=True)
     ctx.close()
     return 0
