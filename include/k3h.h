@@ -153,10 +153,12 @@ K3H_API int k3h_moe_finalize(k3h_ctx_t ctx, void* stream, int topk, const void* 
 /* k3h_moe_permute_mx: no reference entry (moe_fc1 gathers through route_map
  * inside the GEMM, ops.moe_fc1 json:405185).  pq[r] = q[route_map[r]] (cols
  * e4m3 bytes), psf[r] = sf[route_map[r]] (cols/32 E8M0 bytes) for
- * r < *total_padded (a device value).  Persistent grid 2048 x 256; cols % 512 == 0. */
+ * r < min(*total_padded, max_rows); *total_padded is a device value and pq / psf
+ * hold max_rows rows (size them by the route_map capacity, T*topk + E*127, to
+ * cover every routing).  Grid ceil(max_rows/4) x 256; cols % 1024 == 0, <= 16384. */
 K3H_API int k3h_moe_permute_mx(k3h_ctx_t ctx, void* stream, const void* q, const void* sf,
-                               const int* route_map, const int* total_padded, int cols, void* pq,
-                               void* psf);
+                               const int* route_map, const int* total_padded, int max_rows,
+                               int cols, void* pq, void* psf);
 /* kern_k3_moe_w_shuffle / kern_k3_moe_sf_shuffle (k3_moe_prefill_v4.cu:310,320):
  * load-time weight / scale layouts of the grouped GEMM. */
 K3H_API int k3h_moe_w_shuffle(k3h_ctx_t ctx, void* stream, const void* src, void* dst,

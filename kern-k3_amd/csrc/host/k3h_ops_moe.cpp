@@ -109,16 +109,17 @@ K3H_API int k3h_moe_finalize(k3h_ctx_t ctx, void* stream, int topk, const void* 
 }
 
 K3H_API int k3h_moe_permute_mx(k3h_ctx_t ctx, void* stream, const void* q, const void* sf,
-                               const int* route_map, const int* total_padded, int cols, void* pq,
-                               void* psf) {
-  if (!ctx || cols <= 0 || cols % 512) return K3H_EINVAL;
+                               const int* route_map, const int* total_padded, int max_rows,
+                               int cols, void* pq, void* psf) {
+  if (!ctx || cols <= 0 || cols % 1024 || cols > 16384 || max_rows < 0) return K3H_EINVAL;
+  if (max_rows == 0) return K3H_OK;
   if (!k3h_okp(q, 16) || !k3h_okp(sf, 4) || !k3h_okp(route_map, 4) || !k3h_okp(total_padded, 4) ||
       !k3h_okp(pq, 16) || !k3h_okp(psf, 4))
     return K3H_EINVAL;
   K3hArgs a;
-  a.ptr(q).ptr(sf).ptr(route_map).ptr(total_padded).i32(cols).ptr(pq).ptr(psf);
-  // persistent: 2048 workgroups of 4 waves, one row per wave per step
-  return k3h_run(ctx, kMoeV4, "k3h_moe_permute_mx", 2048, 1, 1, 256, stream, a);
+  a.ptr(q).ptr(sf).ptr(route_map).ptr(total_padded).i32(max_rows).i32(cols).ptr(pq).ptr(psf);
+  // one row per wave over max_rows; rows past *total_padded exit
+  return k3h_run(ctx, kMoeV4, "k3h_moe_permute_mx", k3h_cdiv(max_rows, 4), 1, 1, 256, stream, a);
 }
 
 K3H_API int k3h_moe_w_shuffle(k3h_ctx_t ctx, void* stream, const void* src, void* dst,

@@ -18,9 +18,10 @@
 // otherwise the run-time `tile`), SCATTER_WARPS (block 32 * SCATTER_WARPS).
 //
 // Plus one operator with no reference entry (module key k3_moe_prefill_v4+...):
-//   k3h_moe_permute_mx(q, sf, route_map, total_padded, cols, pq, psf)
-//       persistent grid, block 256: pq[r] = q[route_map[r]], psf[r] = sf[route_map[r]]
-//       for r < *total_padded (the reference gathers these rows inside moe_fc1).
+//   k3h_moe_permute_mx(q, sf, route_map, total_padded, max_rows, cols, pq, psf)
+//       grid ceil(max_rows / 4), block 256: pq[r] = q[route_map[r]],
+//       psf[r] = sf[route_map[r]] for r < min(*total_padded, max_rows) (the
+//       reference gathers these rows inside moe_fc1).
 #include "k3_mx.h"
 
 #ifndef TOPK
@@ -245,8 +246,11 @@ extern "C" __global__ void __launch_bounds__(32 * SCATTER_WARPS) kern_k3_moe_rou
 // ascending of wts[t][k] * f32(fc2[exp2perm[t TOPK + k], c])) over the local
 // slots, f32 accumulator from 0, one fma per term.  Manifest geometry: grid
 // ceil(T / 2), block 128, so each wave owns one token: lanes < TOPK read the
-// token's slots, a ballot compacts the local ones, and the wave walks the row
-// two 16-byte vectors per lane at a time.
+// token's slots and a ballot compacts the local ones (k ascending).  The row is
+// walked FV 16-byte vectors per lane at a time; the loads of up to four slots x
+// FV vectors are issued before their fmas, which then run in slot order.
+#define FV 4
+#define FS 4
 extern "C" __global__ void __launch_bounds__(128) kern_k3_moe_finalize(
     const uint16_t* __restrict__ fc2, const int* __restrict__ exp2perm,
     const float* __restrict__ wts, uint16_t* __restrict__ out, int T, int cols) {
@@ -261,7 +265,6 @@ extern "C" __global__ void __launch_bounds__(128) kern_k3_moe_finalize(
   }
   const uint64_t live = __ballot(p >= 0);
   const int n = __builtin_popcountll(live);
-  // compacted slot i = the i-th local k (ascending)
   int srow[TOPK];
   float sw[TOPK];
   {
@@ -269,63 +272,87 @@ extern "C" __global__ void __launch_bounds__(128) kern_k3_moe_finalize(
 #pragma unroll
     for (int i = 0; i < TOPK; ++i) {
       const int k = m ? __builtin_ctzll(m) : 0;
-      srow[i] = __shfl(p, k, 64);
-      sw[i] = __shfl(w, k, 64);
+      srow[i] = __builtin_amdgcn_readfirstlane(__shfl(p, k, 64));
+      sw[i] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(__shfl(w, k, 64))));
       m &= m - 1;
     }
   }
   const int nvec = cols >> 3;  // 16-byte vectors per row
   uint16_t* __restrict__ orow = out + (size_t)t * cols;
-  for (int v0 = lane; v0 < nvec; v0 += 128) {
-    const int v1 = v0 + 64;
-    const bool has1 = v1 < nvec;
-    float a0[8], a1[8];
+  for (int v0 = lane; v0 < nvec; v0 += 64 * FV) {
+    float acc[FV][8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) { a0[j] = 0.0f; a1[j] = 0.0f; }
-    for (int i = 0; i < n; ++i) {
-      const uint16_t* src = fc2 + (size_t)srow[i] * cols;
-      const k3_u4 x0 = k3_ld16(src + (size_t)v0 * 8);
-      const k3_u4 x1 = has1 ? k3_ld16(src + (size_t)v1 * 8) : k3_u4{0, 0, 0, 0};
+    for (int c = 0; c < FV; ++c)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        a0[2 * j] = __builtin_fmaf(sw[i], k3_bf_lo(x0[j]), a0[2 * j]);
-        a0[2 * j + 1] = __builtin_fmaf(sw[i], k3_bf_hi(x0[j]), a0[2 * j + 1]);
-        a1[2 * j] = __builtin_fmaf(sw[i], k3_bf_lo(x1[j]), a1[2 * j]);
-        a1[2 * j + 1] = __builtin_fmaf(sw[i], k3_bf_hi(x1[j]), a1[2 * j + 1]);
+      for (int j = 0; j < 8; ++j) acc[c][j] = 0.0f;
+#pragma unroll
+    for (int i0 = 0; i0 < TOPK; i0 += FS) {
+      if (i0 >= n) break;
+      k3_u4 x[FS][FV];
+#pragma unroll
+      for (int i = 0; i < FS; ++i)
+#pragma unroll
+        for (int c = 0; c < FV; ++c) {
+          const int v = v0 + 64 * c;
+          x[i][c] = (i0 + i < n && v < nvec)
+                        ? k3_ld16(fc2 + (size_t)srow[i0 + i] * cols + (size_t)v * 8)
+                        : k3_u4{0, 0, 0, 0};
+        }
+#pragma unroll
+      for (int i = 0; i < FS; ++i) {
+        if (i0 + i >= n) break;
+        const float wi = sw[i0 + i];
+#pragma unroll
+        for (int c = 0; c < FV; ++c)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            acc[c][2 * j] = __builtin_fmaf(wi, k3_bf_lo(x[i][c][j]), acc[c][2 * j]);
+            acc[c][2 * j + 1] = __builtin_fmaf(wi, k3_bf_hi(x[i][c][j]), acc[c][2 * j + 1]);
+          }
       }
     }
-    k3_u4 o0, o1;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      o0[j] = k3_pack_bf2(a0[2 * j], a0[2 * j + 1]);
-      o1[j] = k3_pack_bf2(a1[2 * j], a1[2 * j + 1]);
+    for (int c = 0; c < FV; ++c) {
+      const int v = v0 + 64 * c;
+      if (v < nvec) {
+        k3_u4 o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = k3_pack_bf2(acc[c][2 * j], acc[c][2 * j + 1]);
+        k3_st16_nt(orow + (size_t)v * 8, o);
+      }
     }
-    k3_st16_nt(orow + (size_t)v0 * 8, o0);
-    if (has1) k3_st16_nt(orow + (size_t)v1 * 8, o1);
   }
 }
 
 // MXFP8 permute: rows of the token-major MXFP8 activation gathered into the
 // expert-contiguous order of route_map (padding rows carry token 0, as routed).
-// Persistent: each wave copies whole rows, r = wave id + k * waves in the grid,
-// until *total_padded; per row 7168 payload bytes (7 x 16 B per lane at cols
-// 7168) and cols / 32 scale bytes.  cols % 512 == 0.
+// One row per wave (r = global wave id, striding by the grid's waves), rows
+// r >= *total_padded exit; all of a row's loads are issued before its stores.
+// Per row cols payload bytes (cols / 1024 16-byte vectors per lane) and cols / 32
+// scale bytes (one word per lane).  cols % 1024 == 0, cols <= 16384.
+#define PM_MAXV 16
 extern "C" __global__ void __launch_bounds__(256) k3h_moe_permute_mx(
     const uint8_t* __restrict__ q, const uint8_t* __restrict__ sf, const int* __restrict__ route_map,
-    const int* __restrict__ total_padded, int cols, uint8_t* __restrict__ pq, uint8_t* __restrict__ psf) {
+    const int* __restrict__ total_padded, int max_rows, int cols, uint8_t* __restrict__ pq,
+    uint8_t* __restrict__ psf) {
   const int lane = threadIdx.x & 63;
-  const int nrows = total_padded[0];
+  const int nrows = min(total_padded[0], max_rows);  // pq / psf hold max_rows rows
   const int nwaves = gridDim.x * (blockDim.x >> 6);
-  const int nv = cols >> 4;          // 16-byte payload vectors per row
-  const int sfb = cols >> 5;         // scale bytes per row
+  const int nv = cols >> 10;   // 16-byte vectors per lane
+  const int sfw = cols >> 7;   // scale words per row
   for (int r = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); r < nrows; r += nwaves) {
     const int t = route_map[r];
     const uint8_t* src = q + (size_t)t * cols;
     uint8_t* dst = pq + (size_t)r * cols;
-    for (int v = lane; v < nv; v += 64) k3_st16_nt(dst + (size_t)v * 16, k3_ld16(src + (size_t)v * 16));
-    const uint8_t* ssrc = sf + (size_t)t * sfb;
-    uint8_t* sdst = psf + (size_t)r * sfb;
-    for (int i = lane * 4; i < sfb; i += 256) *(uint32_t*)(sdst + i) = *(const uint32_t*)(ssrc + i);
+    k3_u4 v[PM_MAXV];
+#pragma unroll
+    for (int k = 0; k < PM_MAXV; ++k)
+      if (k < nv) v[k] = k3_ld16_nt(src + (size_t)(lane + 64 * k) * 16);
+    const uint32_t sw = lane < sfw ? *(const uint32_t*)(sf + (size_t)t * (cols >> 5) + 4 * lane) : 0u;
+#pragma unroll
+    for (int k = 0; k < PM_MAXV; ++k)
+      if (k < nv) k3_st16_nt(dst + (size_t)(lane + 64 * k) * 16, v[k]);
+    if (lane < sfw) *(uint32_t*)(psf + (size_t)r * (cols >> 5) + 4 * lane) = sw;
   }
 }
 

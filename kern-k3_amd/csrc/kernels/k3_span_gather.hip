@@ -21,10 +21,16 @@
 // blockIdx.y == 3: span_beta[h*span + i] = bf16(wsm[at+i, h]) for h < HEADS and
 // span_flow[i, 0..128) = bf16(wsm[at+i, 96..224)) (k3_span_gather_v3.cu:267-281).
 //
-// Each thread owns 4 consecutive columns and 16 rows, loaded 4 rows at a time
-// with the three taps carried in registers.  The logistic uses the hardware 2^x
-// and reciprocal (as the reference's fast form does); the result is within one
-// bf16 ulp of the CPU checker's exact logistic.
+// Work split: a workgroup's tile is 512 columns x 16 rows of one stream; thread
+// t owns 8 consecutive columns (one 16-byte vector per row) and one 8-row half
+// of the tile (threads 0-63 rows 0-7, 64-127 rows 8-15).  All 11 rows a thread
+// needs (its 8 rows and 3 taps) are loaded before any is used.  The second
+// half's taps are the first half's last rows, so their re-read hits L2.  Only
+// the first half of the z == 0 workgroup reads the old window, and it writes
+// the new one after those reads.  beta / flow (y == 3) are landed once, by the
+// x == 0 workgroups.  The logistic uses the hardware 2^x and reciprocal (as the
+// reference's fast form does); the result is within one bf16 ulp of the CPU
+// checker's exact logistic.
 #include "../common/k3_dev.h"
 
 #ifndef HEADS
@@ -37,30 +43,30 @@
 #define K9_WSM 256
 #define K9_WSM_FA 96
 #define K9_ROWS 16
-#define K9_CHUNK 4
-
-K3_DEV void k9_unpack4(k3_u2 w, float* x) {
-  x[0] = k3_bf_lo(w[0]); x[1] = k3_bf_hi(w[0]);
-  x[2] = k3_bf_lo(w[1]); x[3] = k3_bf_hi(w[1]);
-}
-K3_DEV k3_u2 k9_ld4(const uint16_t* p) { return *(const k3_u2*)p; }
 
 K3_DEV float k9_silu(float sb) { return sb * k3_sigmoid_fast(sb); }
 
-K3_DEV k3_u2 k9_row(const float* t0, const float* t1, const float* t2, const float* x,
-                    const float (*w)[4]) {
-  float o[4];
+// One output vector (8 columns) from taps t0..t2 and input x (raw bf16 words).
+K3_DEV k3_u4 k9_row(k3_u4 t0, k3_u4 t1, k3_u4 t2, k3_u4 x, const float (*w)[8]) {
+  k3_u4 r;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    float y = t0[k] * w[0][k];
-    y = __builtin_fmaf(t1[k], w[1][k], y);
-    y = __builtin_fmaf(t2[k], w[2][k], y);
-    y = __builtin_fmaf(x[k], w[3][k], y);
-    o[k] = k9_silu(k3_land(y));
+    float o[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int e = 2 * k + h;
+      const float a0 = h ? k3_bf_hi(t0[k]) : k3_bf_lo(t0[k]);
+      const float a1 = h ? k3_bf_hi(t1[k]) : k3_bf_lo(t1[k]);
+      const float a2 = h ? k3_bf_hi(t2[k]) : k3_bf_lo(t2[k]);
+      const float a3 = h ? k3_bf_hi(x[k]) : k3_bf_lo(x[k]);
+      float y = a0 * w[0][e];
+      y = __builtin_fmaf(a1, w[1][e], y);
+      y = __builtin_fmaf(a2, w[2][e], y);
+      y = __builtin_fmaf(a3, w[3][e], y);
+      o[h] = k9_silu(k3_land(y));
+    }
+    r[k] = k3_pack_bf2(o[0], o[1]);
   }
-  k3_u2 r;
-  r[0] = k3_pack_bf2(o[0], o[1]);
-  r[1] = k3_pack_bf2(o[2], o[3]);
   return r;
 }
 
@@ -71,14 +77,15 @@ extern "C" __global__ void __launch_bounds__(128) kern_k3_span_gather(
     uint16_t* __restrict__ span_beta, uint16_t* __restrict__ span_flow,
     const int* __restrict__ span_at, int span) {
   const int at = span_at[0];
-  const int row0 = blockIdx.z * K9_ROWS;
-  if (row0 >= span) return;
+  const int tile0 = blockIdx.z * K9_ROWS;
+  if (tile0 >= span) return;
   partial += (size_t)at * K9_KDA_FUSED;
   wsm_partial += (size_t)at * K9_WSM;
 
   if (blockIdx.y == 3) {
+    if (blockIdx.x != 0) return;  // the six x workgroups would land identical values
     // 8 threads per row: thread k lands beta for heads k, k + 8, ... and 16 flow columns
-    const int i = row0 + (int)(threadIdx.x / 8), k = threadIdx.x % 8;
+    const int i = tile0 + (int)(threadIdx.x / 8), k = threadIdx.x % 8;
     if (i >= span) return;
     const float* row = wsm_partial + (size_t)i * K9_WSM;
     for (int h = k; h < HEADS; h += 8) span_beta[(size_t)h * span + i] = (uint16_t)k3_pack_bf2(row[h], 0.0f);
@@ -95,55 +102,48 @@ extern "C" __global__ void __launch_bounds__(128) kern_k3_span_gather(
   }
 
   const int s = blockIdx.y;
-  const int c = (int)(blockIdx.x * 128 + threadIdx.x) * 4;
+  const int half = threadIdx.x >> 6;
+  const int c = (int)(blockIdx.x * 64 + (threadIdx.x & 63)) * 8;
+  const int row0 = tile0 + half * 8;
+  if (row0 >= span) return;
+  const int nrow = min(8, span - row0);
   uint16_t* __restrict__ out = s == 0 ? span_q : s == 1 ? span_k : span_v;
+  const uint16_t* __restrict__ col = partial + (size_t)s * K9_INNER + c;
+  const bool first = blockIdx.z == 0 && half == 0;
   uint16_t* win = (uint16_t*)((char*)kda_base + (long long)line_index[at] * line_bytes +
                               K9_REC_BYTES + (long long)s * K9_WIN_BYTES);
-  float w[4][4];
+
+  // x[j] = input row row0 - 3 + j (j < 3: taps), loaded before any use
+  k3_u4 x[11];
+#pragma unroll
+  for (int t = 0; t < 3; ++t)
+    x[t] = first ? k3_ld16(win + (size_t)t * K9_INNER + c)
+                 : k3_ld16(col + (size_t)(row0 - 3 + t) * K9_KDA_FUSED);
+#pragma unroll
+  for (int r = 0; r < 8; ++r)
+    x[3 + r] = k3_ld16_nt(col + (size_t)(row0 + min(r, nrow - 1)) * K9_KDA_FUSED);
+  float w[4][8];
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    const float4 v = *(const float4*)(cw + (size_t)s * 4 * K9_INNER + (size_t)t * K9_INNER + c);
-    w[t][0] = v.x; w[t][1] = v.y; w[t][2] = v.z; w[t][3] = v.w;
+    const float4* wp = (const float4*)(cw + (size_t)s * 4 * K9_INNER + (size_t)t * K9_INNER + c);
+    const float4 a = wp[0], b = wp[1];
+    w[t][0] = a.x; w[t][1] = a.y; w[t][2] = a.z; w[t][3] = a.w;
+    w[t][4] = b.x; w[t][5] = b.y; w[t][6] = b.z; w[t][7] = b.w;
   }
-  const uint16_t* __restrict__ col = partial + (size_t)s * K9_INNER + c;
-
-  // x[j] = input row row0 - 3 + j
-  float x[K9_CHUNK + 3][4];
-  const bool first = blockIdx.z == 0;
 #pragma unroll
-  for (int t = 0; t < 3; ++t) {
-    if (first) k9_unpack4(k9_ld4(win + (size_t)t * K9_INNER + c), x[t]);
-    else k9_unpack4(k9_ld4(col + (size_t)(row0 - 3 + t) * K9_KDA_FUSED), x[t]);
-  }
-  const int rend = min(row0 + K9_ROWS, span);
-  for (int r0 = row0; r0 < rend; r0 += K9_CHUNK) {
-    k3_u2 raw[K9_CHUNK];
-#pragma unroll
-    for (int r = 0; r < K9_CHUNK; ++r)
-      if (r0 + r < rend) raw[r] = k9_ld4(col + (size_t)(r0 + r) * K9_KDA_FUSED);
-#pragma unroll
-    for (int r = 0; r < K9_CHUNK; ++r) {
-      if (r0 + r < rend) {
-        k9_unpack4(raw[r], x[3 + r]);
-        *(k3_u2*)(out + (size_t)(r0 + r) * K9_INNER + c) = k9_row(x[r], x[r + 1], x[r + 2], x[r + 3], w);
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < 3; ++t)
-#pragma unroll
-      for (int k = 0; k < 4; ++k) x[t][k] = x[K9_CHUNK + t][k];
-  }
+  for (int r = 0; r < 8; ++r)
+    if (r < nrow) k3_st16_nt(out + (size_t)(row0 + r) * K9_INNER + c, k9_row(x[r], x[r + 1], x[r + 2], x[r + 3], w));
 
   if (first) {
-    // new window = x_{span-3 .. span-1}; all reads of the old window are done
-    k3_u2 nt[3];
+    // new window = x_{span-3 .. span-1}; this thread's old-window reads are done
+    k3_u4 nt[3];
 #pragma unroll
     for (int t = 0; t < 3; ++t) {
       const int i = span - 3 + t;
-      nt[t] = i < 0 ? k9_ld4(win + (size_t)(i + 3) * K9_INNER + c)
-                    : k9_ld4(col + (size_t)i * K9_KDA_FUSED);
+      // i < 0 (span < 3): old window row i + 3, still in x[0..2]
+      nt[t] = i >= 0 ? k3_ld16(col + (size_t)i * K9_KDA_FUSED) : i == -3 ? x[0] : i == -2 ? x[1] : x[2];
     }
 #pragma unroll
-    for (int t = 0; t < 3; ++t) *(k3_u2*)(win + (size_t)t * K9_INNER + c) = nt[t];
+    for (int t = 0; t < 3; ++t) k3_st16(win + (size_t)t * K9_INNER + c, nt[t]);
   }
 }

@@ -75,7 +75,7 @@ _SIGS: dict[str, list] = {
     "k3h_moe_route_tables": [_P, _P, _P, _I, _I, _I, _P, _P, _P, _P, _P, _P],
     "k3h_moe_route_scatter": [_P, _P, _I, _P, _P, _I, _I, _I, _P, _P],
     "k3h_moe_finalize": [_P, _P, _I, _P, _P, _P, _P, _I, _I],
-    "k3h_moe_permute_mx": [_P, _P, _P, _P, _P, _P, _I, _P, _P],
+    "k3h_moe_permute_mx": [_P, _P, _P, _P, _P, _P, _I, _I, _P, _P],
     "k3h_moe_w_shuffle": [_P, _P, _P, _P, _I, _I, _I, _I],
     "k3h_moe_sf_shuffle": [_P, _P, _P, _P, _I, _I, _I, _I],
     "k3h_span_gather": [_P, _P, _P, _P, _P, _P, ctypes.c_int64, _P, _P, _P, _P, _P, _P, _P, _I],
@@ -336,15 +336,19 @@ class Ctx:
         _check(self.L.k3h_moe_finalize(self.h, _stream(stream), topk, _ptr(fc2), _ptr(exp2perm),
                                        _ptr(wts), _ptr(out), T, cols), "moe_finalize")
 
-    def moe_permute_mx(self, q, sf, route_map, total_padded, cols: int, pq, psf, stream=None) -> None:
+    def moe_permute_mx(self, q, sf, route_map, total_padded, cols: int, pq, psf,
+                       stream=None) -> None:
+        """pq[r] = q[route_map[r]], psf[r] = sf[route_map[r]] for r < total_padded[0]
+        (a device value), at most the rows pq / psf hold."""
+        max_rows = min(pq.numel() // cols, psf.numel() // (cols // 32), route_map.numel())
         _dev(q, "q", U8, cols)
         _dev(sf, "sf", U8, cols // 32, align=4)
         _dev(route_map, "route_map", I32, 1, align=4)
         _dev(total_padded, "total_padded", I32, 1, align=4)
-        _dev(pq, "pq", U8, cols)
-        _dev(psf, "psf", U8, cols // 32, align=4)
+        _dev(pq, "pq", U8, 1)
+        _dev(psf, "psf", U8, 1, align=4)
         _check(self.L.k3h_moe_permute_mx(self.h, _stream(stream), _ptr(q), _ptr(sf), _ptr(route_map),
-                                         _ptr(total_padded), cols, _ptr(pq), _ptr(psf)),
+                                         _ptr(total_padded), max_rows, cols, _ptr(pq), _ptr(psf)),
                "moe_permute_mx")
 
     def moe_w_shuffle(self, src, dst, experts: int, n: int, row_bytes: int, gated: int,
