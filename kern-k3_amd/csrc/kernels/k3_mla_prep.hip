@@ -40,19 +40,31 @@
 #define PG_COLS (INNER / PG_THREADS)
 #define PH_ROWS 4
 #define PH_THREADS (PH_ROWS * 128)
+#ifndef MLA_NT
+#define MLA_NT 1  // partial rows are read once: non-temporal loads
+#endif
 
 #ifdef K3_MLA_BF16
 typedef uint16_t k3_mla_t;
 // four consecutive partial values of a row, landed (bf16 input: exact)
 K3_DEV float4 k3_mla_ld4(const k3_mla_t* p) {
+#if MLA_NT
+  const k3_u2 w = __builtin_nontemporal_load((const k3_u2*)p);
+#else
   const k3_u2 w = *(const k3_u2*)p;
+#endif
   return make_float4(k3_bf_lo(w[0]), k3_bf_hi(w[0]), k3_bf_lo(w[1]), k3_bf_hi(w[1]));
 }
 #else
 typedef float k3_mla_t;
 K3_DEV float4 k3_mla_ld4(const k3_mla_t* p) {
-  const float4 v = *(const float4*)p;
-  return make_float4(k3_land(v.x), k3_land(v.y), k3_land(v.z), k3_land(v.w));
+#if MLA_NT
+  const k3_u4 u = k3_ld16_nt(p);
+#else
+  const k3_u4 u = k3_ld16(p);
+#endif
+  return make_float4(k3_land(__uint_as_float(u[0])), k3_land(__uint_as_float(u[1])),
+                     k3_land(__uint_as_float(u[2])), k3_land(__uint_as_float(u[3])));
 }
 #endif
 
@@ -81,11 +93,15 @@ extern "C" __global__ void __launch_bounds__(PG_THREADS) kern_k3_mla_prep_gate(
   for (int r = 0; r < PG_ROWS; ++r) {
     const int b = min(r0 + r, B - 1);  // loads stay in bounds; stores are predicated
     const k3_mla_t* src = partial + (size_t)b * MLA_FUSED + HEADC + c;
-    const float4 a = k3_mla_ld4(src), d = k3_mla_ld4(src + 4);
-    o[r][0] = k3_pack_bf2(a.x, a.y);
-    o[r][1] = k3_pack_bf2(a.z, a.w);
-    o[r][2] = k3_pack_bf2(d.x, d.y);
-    o[r][3] = k3_pack_bf2(d.z, d.w);
+#ifdef K3_MLA_BF16
+    o[r] = k3_ld16_nt(src);  // already bf16: the landing is the identity
+#else
+    const k3_u4 a = k3_ld16_nt(src), d = k3_ld16_nt(src + 4);
+    o[r][0] = k3_pack_bf2(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    o[r][1] = k3_pack_bf2(__uint_as_float(a[2]), __uint_as_float(a[3]));
+    o[r][2] = k3_pack_bf2(__uint_as_float(d[0]), __uint_as_float(d[1]));
+    o[r][3] = k3_pack_bf2(__uint_as_float(d[2]), __uint_as_float(d[3]));
+#endif
   }
 #pragma unroll
   for (int r = 0; r < PG_ROWS; ++r)

@@ -249,8 +249,15 @@ extern "C" __global__ void __launch_bounds__(32 * SCATTER_WARPS) kern_k3_moe_rou
 // token's slots and a ballot compacts the local ones (k ascending).  The row is
 // walked FV 16-byte vectors per lane at a time; the loads of up to four slots x
 // FV vectors are issued before their fmas, which then run in slot order.
+#ifndef FV
 #define FV 4
-#define FS 4
+#endif
+#ifndef FS
+#define FS 8
+#endif
+#ifndef FIN_NT
+#define FIN_NT 1
+#endif
 extern "C" __global__ void __launch_bounds__(128) kern_k3_moe_finalize(
     const uint16_t* __restrict__ fc2, const int* __restrict__ exp2perm,
     const float* __restrict__ wts, uint16_t* __restrict__ out, int T, int cols) {
@@ -295,7 +302,8 @@ extern "C" __global__ void __launch_bounds__(128) kern_k3_moe_finalize(
         for (int c = 0; c < FV; ++c) {
           const int v = v0 + 64 * c;
           x[i][c] = (i0 + i < n && v < nvec)
-                        ? k3_ld16(fc2 + (size_t)srow[i0 + i] * cols + (size_t)v * 8)
+                        ? (FIN_NT ? k3_ld16_nt(fc2 + (size_t)srow[i0 + i] * cols + (size_t)v * 8)
+                                  : k3_ld16(fc2 + (size_t)srow[i0 + i] * cols + (size_t)v * 8))
                         : k3_u4{0, 0, 0, 0};
         }
 #pragma unroll

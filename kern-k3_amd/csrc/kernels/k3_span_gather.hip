@@ -22,15 +22,15 @@
 // span_flow[i, 0..128) = bf16(wsm[at+i, 96..224)) (k3_span_gather_v3.cu:267-281).
 //
 // Work split: a workgroup's tile is 512 columns x 16 rows of one stream; thread
-// t owns 8 consecutive columns (one 16-byte vector per row) and one 8-row half
-// of the tile (threads 0-63 rows 0-7, 64-127 rows 8-15).  All 11 rows a thread
-// needs (its 8 rows and 3 taps) are loaded before any is used.  The second
-// half's taps are the first half's last rows, so their re-read hits L2.  Only
-// the first half of the z == 0 workgroup reads the old window, and it writes
-// the new one after those reads.  beta / flow (y == 3) are landed once, by the
-// x == 0 workgroups.  The logistic uses the hardware 2^x and reciprocal (as the
-// reference's fast form does); the result is within one bf16 ulp of the CPU
-// checker's exact logistic.
+// t owns 4 consecutive columns (one 8-byte vector per row) for all 16 rows, so
+// only 3 tap rows per 16 are read twice.  All 19 row vectors and the weights are
+// loaded (non-temporally) before any is used.  On MI355X this tile shape moves
+// the span's bytes faster than 16-byte vectors over 8-row halves (6 tap rows
+// per 16) and faster than any cacheable tap load.  Only the z == 0 workgroup
+// reads the old window, and it writes the new one after those reads.  beta /
+// flow (y == 3) are landed once, by the x == 0 workgroups.  The logistic uses the
+// hardware 2^x and reciprocal (as the reference's fast form does); the result is
+// within one bf16 ulp of the CPU checker's exact logistic.
 #include "../common/k3_dev.h"
 
 #ifndef HEADS
@@ -46,29 +46,34 @@
 
 K3_DEV float k9_silu(float sb) { return sb * k3_sigmoid_fast(sb); }
 
-// One output vector (8 columns) from taps t0..t2 and input x (raw bf16 words).
-K3_DEV k3_u4 k9_row(k3_u4 t0, k3_u4 t1, k3_u4 t2, k3_u4 x, const float (*w)[8]) {
-  k3_u4 r;
+K3_DEV void k9_unpack4(k3_u2 v, float* a) {
+  a[0] = k3_bf_lo(v[0]); a[1] = k3_bf_hi(v[0]);
+  a[2] = k3_bf_lo(v[1]); a[3] = k3_bf_hi(v[1]);
+}
+
+// One output vector (4 columns) from unpacked taps a0..a2 and input a3: conv fma
+// chain, one bf16 landing per pair of values, SiLU, bf16 pack.
+K3_DEV k3_u2 k9_row(const float* a0, const float* a1, const float* a2, const float* a3,
+                    const float (*w)[4]) {
+  k3_u2 r;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    float o[2];
+  for (int k = 0; k < 2; ++k) {
+    float y[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int e = 2 * k + h;
-      const float a0 = h ? k3_bf_hi(t0[k]) : k3_bf_lo(t0[k]);
-      const float a1 = h ? k3_bf_hi(t1[k]) : k3_bf_lo(t1[k]);
-      const float a2 = h ? k3_bf_hi(t2[k]) : k3_bf_lo(t2[k]);
-      const float a3 = h ? k3_bf_hi(x[k]) : k3_bf_lo(x[k]);
-      float y = a0 * w[0][e];
-      y = __builtin_fmaf(a1, w[1][e], y);
-      y = __builtin_fmaf(a2, w[2][e], y);
-      y = __builtin_fmaf(a3, w[3][e], y);
-      o[h] = k9_silu(k3_land(y));
+      float v = a0[e] * w[0][e];
+      v = __builtin_fmaf(a1[e], w[1][e], v);
+      v = __builtin_fmaf(a2[e], w[2][e], v);
+      y[h] = __builtin_fmaf(a3[e], w[3][e], v);
     }
-    r[k] = k3_pack_bf2(o[0], o[1]);
+    const uint32_t sb = k3_pack_bf2(y[0], y[1]);
+    r[k] = k3_pack_bf2(k9_silu(k3_bf_lo(sb)), k9_silu(k3_bf_hi(sb)));
   }
   return r;
 }
+
+K3_DEV k3_u2 k9_ld8_nt(const uint16_t* p) { return __builtin_nontemporal_load((const k3_u2*)p); }
 
 extern "C" __global__ void __launch_bounds__(128) kern_k3_span_gather(
     const uint16_t* __restrict__ partial, const float* __restrict__ cw, void* __restrict__ kda_base,
@@ -76,14 +81,18 @@ extern "C" __global__ void __launch_bounds__(128) kern_k3_span_gather(
     uint16_t* __restrict__ span_q, uint16_t* __restrict__ span_k, uint16_t* __restrict__ span_v,
     uint16_t* __restrict__ span_beta, uint16_t* __restrict__ span_flow,
     const int* __restrict__ span_at, int span) {
+  // Tiles in launch order: the tile above (z - 1) was dispatched 24 workgroups
+  // earlier, i.e. to the same XCD (round-robin over 8), so its tap rows are read
+  // through the same L2.
+  const uint32_t bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
   const int at = span_at[0];
-  const int tile0 = blockIdx.z * K9_ROWS;
+  const int tile0 = bz * K9_ROWS;
   if (tile0 >= span) return;
   partial += (size_t)at * K9_KDA_FUSED;
   wsm_partial += (size_t)at * K9_WSM;
 
-  if (blockIdx.y == 3) {
-    if (blockIdx.x != 0) return;  // the six x workgroups would land identical values
+  if (by == 3) {
+    if (bx != 0) return;  // the six x workgroups would land identical values
     // 8 threads per row: thread k lands beta for heads k, k + 8, ... and 16 flow columns
     const int i = tile0 + (int)(threadIdx.x / 8), k = threadIdx.x % 8;
     if (i >= span) return;
@@ -101,49 +110,56 @@ extern "C" __global__ void __launch_bounds__(128) kern_k3_span_gather(
     return;
   }
 
-  const int s = blockIdx.y;
-  const int half = threadIdx.x >> 6;
-  const int c = (int)(blockIdx.x * 64 + (threadIdx.x & 63)) * 8;
-  const int row0 = tile0 + half * 8;
-  if (row0 >= span) return;
-  const int nrow = min(8, span - row0);
+  const int s = by;
+  const int c = (int)(bx * 128 + threadIdx.x) * 4;
+  const int row0 = tile0;
+  const int nrow = min(K9_ROWS, span - row0);
   uint16_t* __restrict__ out = s == 0 ? span_q : s == 1 ? span_k : span_v;
   const uint16_t* __restrict__ col = partial + (size_t)s * K9_INNER + c;
-  const bool first = blockIdx.z == 0 && half == 0;
+  const bool first = bz == 0;
   uint16_t* win = (uint16_t*)((char*)kda_base + (long long)line_index[at] * line_bytes +
                               K9_REC_BYTES + (long long)s * K9_WIN_BYTES);
 
-  // x[j] = input row row0 - 3 + j (j < 3: taps), loaded before any use
-  k3_u4 x[11];
-#pragma unroll
-  for (int t = 0; t < 3; ++t)
-    x[t] = first ? k3_ld16(win + (size_t)t * K9_INNER + c)
-                 : k3_ld16(col + (size_t)(row0 - 3 + t) * K9_KDA_FUSED);
-#pragma unroll
-  for (int r = 0; r < 8; ++r)
-    x[3 + r] = k3_ld16_nt(col + (size_t)(row0 + min(r, nrow - 1)) * K9_KDA_FUSED);
-  float w[4][8];
+  // Loads in first-use order (weights, taps, rows), all issued before any use.
+  float w[4][4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    const float4* wp = (const float4*)(cw + (size_t)s * 4 * K9_INNER + (size_t)t * K9_INNER + c);
-    const float4 a = wp[0], b = wp[1];
-    w[t][0] = a.x; w[t][1] = a.y; w[t][2] = a.z; w[t][3] = a.w;
-    w[t][4] = b.x; w[t][5] = b.y; w[t][6] = b.z; w[t][7] = b.w;
-  }
+    const k3_u4 a = k3_ld16(cw + (size_t)s * 4 * K9_INNER + (size_t)t * K9_INNER + c);
 #pragma unroll
-  for (int r = 0; r < 8; ++r)
-    if (r < nrow) k3_st16_nt(out + (size_t)(row0 + r) * K9_INNER + c, k9_row(x[r], x[r + 1], x[r + 2], x[r + 3], w));
+    for (int k = 0; k < 4; ++k) w[t][k] = __uint_as_float(a[k]);
+  }
+  // x[j] = input row row0 - 3 + j (j < 3: taps)
+  k3_u2 x[K9_ROWS + 3];
+#pragma unroll
+  for (int t = 0; t < 3; ++t)
+    x[t] = first ? *(const k3_u2*)(win + (size_t)t * K9_INNER + c)
+                 : k9_ld8_nt(col + (size_t)(row0 - 3 + t) * K9_KDA_FUSED);
+#pragma unroll
+  for (int r = 0; r < K9_ROWS; ++r)
+    x[3 + r] = k9_ld8_nt(col + (size_t)(row0 + min(r, nrow - 1)) * K9_KDA_FUSED);
+
+  // slide over the rows: each input row is unpacked once
+  float a[4][4];
+  k9_unpack4(x[0], a[0]);
+  k9_unpack4(x[1], a[1]);
+  k9_unpack4(x[2], a[2]);
+#pragma unroll
+  for (int r = 0; r < K9_ROWS; ++r) {
+    k9_unpack4(x[3 + r], a[(r + 3) & 3]);
+    const k3_u2 o = k9_row(a[r & 3], a[(r + 1) & 3], a[(r + 2) & 3], a[(r + 3) & 3], w);
+    if (r < nrow) __builtin_nontemporal_store(o, (k3_u2*)(out + (size_t)(row0 + r) * K9_INNER + c));
+  }
 
   if (first) {
     // new window = x_{span-3 .. span-1}; this thread's old-window reads are done
-    k3_u4 nt[3];
+    k3_u2 nt[3];
 #pragma unroll
     for (int t = 0; t < 3; ++t) {
       const int i = span - 3 + t;
       // i < 0 (span < 3): old window row i + 3, still in x[0..2]
-      nt[t] = i >= 0 ? k3_ld16(col + (size_t)i * K9_KDA_FUSED) : i == -3 ? x[0] : i == -2 ? x[1] : x[2];
+      nt[t] = i >= 0 ? *(const k3_u2*)(col + (size_t)i * K9_KDA_FUSED) : i == -3 ? x[0] : i == -2 ? x[1] : x[2];
     }
 #pragma unroll
-    for (int t = 0; t < 3; ++t) k3_st16(win + (size_t)t * K9_INNER + c, nt[t]);
+    for (int t = 0; t < 3; ++t) *(k3_u2*)(win + (size_t)t * K9_INNER + c) = nt[t];
   }
 }
