@@ -28,7 +28,7 @@
 // the span's bytes faster than 16-byte vectors over 8-row halves (6 tap rows
 // per 16) and faster than any cacheable tap load.  Only the z == 0 workgroup
 // reads the old window, and it writes the new one after those reads.  beta /
-// flow (y == 3) are landed once, by the x == 0 workgroups.  The logistic uses the
+// flow (y == 3) are landed once per row tile.  The logistic uses the
 // hardware 2^x and reciprocal (as the reference's fast form does); the result is
 // within one bf16 ulp of the CPU checker's exact logistic.
 #include "../common/k3_dev.h"
@@ -43,6 +43,7 @@
 #define K9_WSM 256
 #define K9_WSM_FA 96
 #define K9_ROWS 16
+#define K9_XT (K9_INNER / 512)  // column tiles per stream (gridDim.x)
 
 K3_DEV float k9_silu(float sb) { return sb * k3_sigmoid_fast(sb); }
 
@@ -81,18 +82,31 @@ extern "C" __global__ void __launch_bounds__(128) kern_k3_span_gather(
     uint16_t* __restrict__ span_q, uint16_t* __restrict__ span_k, uint16_t* __restrict__ span_v,
     uint16_t* __restrict__ span_beta, uint16_t* __restrict__ span_flow,
     const int* __restrict__ span_at, int span) {
-  // Tiles in launch order: the tile above (z - 1) was dispatched 24 workgroups
-  // earlier, i.e. to the same XCD (round-robin over 8), so its tap rows are read
-  // through the same L2.
-  const uint32_t bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
+  // Workgroups reach the XCDs round-robin by linear id.  The launch has
+  // 4 * K9_XT workgroups per row tile but only 3 * K9_XT + 1 with work, so the
+  // tiles are renumbered: linear ids [0, 3 K9_XT nz) are the stream tiles
+  // (column tile fastest, then stream, then row tile), the next nz ids the
+  // beta / flow tiles, and the rest exit.  Every XCD then gets the same share.
+  const uint32_t nz = min(gridDim.z, (uint32_t)(span + K9_ROWS - 1) / K9_ROWS);
+  const uint32_t L = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  uint32_t bx, by, bz;
+  if (L < 3 * K9_XT * nz) {
+    bz = L / (3 * K9_XT);
+    by = L % (3 * K9_XT) / K9_XT;
+    bx = L % K9_XT;
+  } else if (L < (3 * K9_XT + 1) * nz) {
+    bz = L - 3 * K9_XT * nz;
+    by = 3;
+    bx = 0;
+  } else {
+    return;
+  }
   const int at = span_at[0];
   const int tile0 = bz * K9_ROWS;
-  if (tile0 >= span) return;
   partial += (size_t)at * K9_KDA_FUSED;
   wsm_partial += (size_t)at * K9_WSM;
 
   if (by == 3) {
-    if (bx != 0) return;  // the six x workgroups would land identical values
     // 8 threads per row: thread k lands beta for heads k, k + 8, ... and 16 flow columns
     const int i = tile0 + (int)(threadIdx.x / 8), k = threadIdx.x % 8;
     if (i >= span) return;
