@@ -98,6 +98,29 @@ K3_DEV uint32_t k3_quad_max_u32(uint32_t v) {
   return v > o ? v : o;
 }
 
+// Wave-wide unsigned max, returned uniform.  GFX9 DPP: quad exchanges, then
+// the half-row and row mirrors make every lane of a 16-lane row hold the row
+// max; row_bcast15 folds row 0 into row 1 and row 2 into row 3, row_bcast31
+// folds rows 0-1 into row 3, whose lane 63 then holds the wave max.  Lanes a
+// broadcast does not write keep 0, the identity of the max.
+#define K3_DPP_ROW_MIRROR 0x140
+#define K3_DPP_ROW_HALF_MIRROR 0x141
+#define K3_DPP_ROW_BCAST15 0x142
+#define K3_DPP_ROW_BCAST31 0x143
+
+K3_DEV uint32_t k3_wave_max_u32_uniform(uint32_t v) {
+  v = k3_quad_max_u32(v);
+  uint32_t o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, K3_DPP_ROW_HALF_MIRROR, 0xf, 0xf, false);
+  v = v > o ? v : o;
+  o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, K3_DPP_ROW_MIRROR, 0xf, 0xf, false);
+  v = v > o ? v : o;
+  o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, K3_DPP_ROW_BCAST15, 0xa, 0xf, false);
+  v = v > o ? v : o;
+  o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, K3_DPP_ROW_BCAST31, 0xc, 0xf, false);
+  v = v > o ? v : o;
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
 // xor swizzle inside 32-lane groups (ds_swizzle bit mode: and 0x1f, xor m).
 template <int M>
 K3_DEV float k3_swz_xor(float v) {

@@ -1,6 +1,7 @@
 // Module k3_router_argmax[+TOPK=n]: MoE router top-k and the two-stage f32 argmax.
 //
 //   kern_k3_router_topk(S, bias, rs, idx, wts, B)      grid (B), block 256
+//   k3h_router_topk_rows(S, bias, rs, idx, wts, B)     grid ceil(B / 4), block 256
 //   kern_k3_argmax_f32_partial(logits, pmax, pidx, n)  grid (B, PARTS), block 1024
 //   kern_k3_argmax_f32_final(pmax, pidx, out, parts)   grid (B), block 64
 //
@@ -17,9 +18,9 @@
 //   butterfly over the TOPK pick lanes (offsets TOPK/2 .. 1).
 // e^x is the deterministic k3_expf, so sig and therefore every key and index
 // are reproduced bit for bit by the CPU checker.  One wave does the row:
-// expert e = lane + 64 j lives in slot j of lane `lane`; a pick is a wave max
-// of the keys followed by a wave min of the matching expert ids.  The other
-// three waves of the manifest's 256-thread block have no work.
+// expert e = lane + 64 j lives in slot j of lane `lane`.  In the manifest
+// geometry the other three waves of the 256-thread block have no work;
+// k3h_router_topk_rows (no reference counterpart) gives each wave a row.
 #include "../common/k3_dev.h"
 
 #define EXPERTS 224
@@ -29,29 +30,12 @@
 #define RSLOTS ((EXPERTS + 63) / 64)  // 4 slots per lane
 static_assert(TOPK >= 1 && TOPK <= 32 && (TOPK & (TOPK - 1)) == 0, "TOPK: power of two <= 32");
 
-K3_DEV uint32_t k3_wave_max_u32(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const uint32_t p = (uint32_t)__shfl_xor((int)v, o, 64);
-    v = v > p ? v : p;
-  }
-  return v;
-}
-K3_DEV uint32_t k3_wave_min_u32(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const uint32_t p = (uint32_t)__shfl_xor((int)v, o, 64);
-    v = v < p ? v : p;
-  }
-  return v;
-}
-
-extern "C" __global__ void __launch_bounds__(256) kern_k3_router_topk(
-    const float* __restrict__ S, const float* __restrict__ bias, const uint16_t* __restrict__ rs,
-    int* __restrict__ idx, float* __restrict__ wts, int B) {
-  const int b = blockIdx.x;
-  if (b >= B || threadIdx.x >= 64) return;
-  const int lane = threadIdx.x;
+// Row b on one full wave.  A pick is a DPP wave max of the keys (uniform) and a
+// ballot per slot for the lanes holding it: slots are scanned from the top so the
+// lowest slot, and in it the lowest lane, i.e. the smallest expert id, wins.
+K3_DEV void k3_router_row(const float* __restrict__ S, const float* __restrict__ bias,
+                          const uint16_t* __restrict__ rs, int* __restrict__ idx,
+                          float* __restrict__ wts, int b, int lane) {
   const float* row = S + (size_t)b * EXPERTS;
 
   uint32_t key[RSLOTS];
@@ -73,18 +57,21 @@ extern "C" __global__ void __launch_bounds__(256) kern_k3_router_topk(
     uint32_t m = key[0];
 #pragma unroll
     for (int j = 1; j < RSLOTS; ++j) m = m > key[j] ? m : key[j];
-    m = k3_wave_max_u32(m);
-    uint32_t mine = 0xffffffffu;
+    m = k3_wave_max_u32_uniform(m);
+    int jw = 0, lw = 0;
 #pragma unroll
-    for (int j = RSLOTS - 1; j >= 0; --j)
-      if (key[j] == m) mine = (uint32_t)(lane + 64 * j);
-    const uint32_t ew = __builtin_amdgcn_readfirstlane(k3_wave_min_u32(mine));
-    float sw = 0.0f;
+    for (int j = RSLOTS - 1; j >= 0; --j) {
+      const unsigned long long mk = __ballot(key[j] == m);
+      if (mk) { jw = j; lw = __builtin_ctzll(mk); }
+    }
+    float sv = sig[0];
+#pragma unroll
+    for (int j = 1; j < RSLOTS; ++j) sv = jw == j ? sig[j] : sv;
+    const float sw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv), lw));
 #pragma unroll
     for (int j = 0; j < RSLOTS; ++j)
-      if ((uint32_t)(lane + 64 * j) == ew) { sw = sig[j]; key[j] = 0u; }
-    sw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sw), (int)(ew & 63u)));
-    if (lane == r) { my_idx = (int)ew; my_sig = sw; }
+      if (j == jw && lane == lw) key[j] = 0u;
+    if (lane == r) { my_idx = 64 * jw + lw; my_sig = sw; }
   }
 
   // renormalise over the TOPK pick lanes: butterfly TOPK/2 .. 1, identical bits on every lane
@@ -96,6 +83,24 @@ extern "C" __global__ void __launch_bounds__(256) kern_k3_router_topk(
     wts[(size_t)b * TOPK + lane] = (my_sig / (den + 1e-20f)) * rsf;
     idx[(size_t)b * TOPK + lane] = my_idx;
   }
+}
+
+// Manifest geometry: one row per 256-thread workgroup, wave 0 does it.
+extern "C" __global__ void __launch_bounds__(256) kern_k3_router_topk(
+    const float* __restrict__ S, const float* __restrict__ bias, const uint16_t* __restrict__ rs,
+    int* __restrict__ idx, float* __restrict__ wts, int B) {
+  const int b = blockIdx.x;
+  if (b >= B || threadIdx.x >= 64) return;
+  k3_router_row(S, bias, rs, idx, wts, b, threadIdx.x);
+}
+
+// Same contract, one row per wave: grid ceil(B / 4), block 256.
+extern "C" __global__ void __launch_bounds__(256) k3h_router_topk_rows(
+    const float* __restrict__ S, const float* __restrict__ bias, const uint16_t* __restrict__ rs,
+    int* __restrict__ idx, float* __restrict__ wts, int B) {
+  const int b = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  if (b >= B) return;
+  k3_router_row(S, bias, rs, idx, wts, b, threadIdx.x & 63);
 }
 
 // ---------------------------------------------------------------- argmax
