@@ -104,14 +104,17 @@ extern "C" __global__ void __launch_bounds__(ROUTE_BLOCK) kern_k3_moe_route_coun
   if ((int)threadIdx.x < E) blockcount[blockIdx.x * E + threadIdx.x] = cnt[threadIdx.x];
 }
 
-// Wave-wide inclusive prefix sum (Hillis-Steele over 64 lanes).
+// Wave-wide inclusive prefix sum of integers, GFX9 DPP: row_shr 1, 2, 4, 8 scan
+// each 16-lane row (lanes without a source add 0), row_bcast15 carries row 0's
+// total into row 1 and row 2's into row 3, row_bcast31 carries rows 0-1 into
+// rows 2-3.
 K3_DEV int k3_wave_incl_scan(int v) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int p = __shfl_up(v, o, 64);
-    if (lane >= o) v += p;
-  }
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, K3_DPP_ROW_BCAST15, 0xa, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, K3_DPP_ROW_BCAST31, 0xc, 0xf, false);
   return v;
 }
 
@@ -119,126 +122,149 @@ K3_DEV int k3_wave_incl_scan(int v) {
 // off = exclusive scan of ceil(count / tile) (CTA units), blockoff[b][e] =
 // tile off[e] + the expert's count in blocks before b, padding rows of an
 // expert's last tile route token 0, cta_batch / cta_limit per CTA index.
-// One workgroup of 16 waves: wave w owns experts w, w + 16, ... and scans the
-// per-block counts across its lanes 64 blocks at a time.
+// One workgroup of 16 waves.  The per-block counts are staged in LDS with
+// coalesced loads (when blocks * E fits); wave w owns experts w, w + 16, ...
+// for the totals, the blockoff scan (64 blocks per DPP scan), the padding rows
+// and the expert's CTA range [off[e], off[e+1]); wave 0 scans the CTA units of
+// all experts (lane = expert).  Staged blockoff values replace the counts in
+// LDS and leave in one coalesced pass.
+#define RT_STAGE 8192  // ints of staged per-block counts (32 KB)
+
 extern "C" __global__ void __launch_bounds__(1024) kern_k3_moe_route_tables(
     const int* __restrict__ blockcount, int blocks, int E, int tile, int* __restrict__ blockoff,
     int* __restrict__ cta_batch, int* __restrict__ cta_limit, int* __restrict__ num_non_exiting,
     int* __restrict__ total_padded, int* __restrict__ route_map) {
+  __shared__ int bc[RT_STAGE];
   __shared__ int count[MAX_E], off[MAX_E + 1];
 #ifdef TILE_SHIFT
   tile = 1 << TILE_SHIFT;
 #endif
+  if (E < 1 || E > MAX_E) {  // no local experts: nothing routed
+    if (threadIdx.x == 0) { num_non_exiting[0] = 0; total_padded[0] = 0; }
+    return;
+  }
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
-  // pass 1: per-expert totals
+  const int n = blocks * E;
+  const bool staged = n <= RT_STAGE;
+  if (staged)
+    for (int i = threadIdx.x; i < n; i += blockDim.x) bc[i] = blockcount[i];
+  __syncthreads();
   for (int e = wave; e < E; e += nw) {
-    int run = 0;
-    for (int b0 = 0; b0 < blocks; b0 += 64) {
-      const int b = b0 + lane;
-      const int c = b < blocks ? blockcount[b * E + e] : 0;
-      run += __shfl(k3_wave_incl_scan(c), 63, 64);
+    int sum = 0;
+    for (int b = lane; b < blocks; b += 64) sum += staged ? bc[b * E + e] : blockcount[b * E + e];
+    sum = __builtin_amdgcn_readlane(k3_wave_incl_scan(sum), 63);
+    if (lane == 0) count[e] = sum;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const int u = lane < E ? (count[lane] + tile - 1) / tile : 0;
+    const int incl = k3_wave_incl_scan(u);
+    if (lane < E) off[lane] = incl - u;
+    if (lane == E - 1) {
+      off[E] = incl;
+      num_non_exiting[0] = incl;
+      total_padded[0] = incl * tile;
     }
-    if (lane == 0) count[e] = run;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int run = 0;
-    for (int j = 0; j < E; ++j) { off[j] = run; run += (count[j] + tile - 1) / tile; }
-    off[E] = run;
-    num_non_exiting[0] = run;
-    total_padded[0] = run * tile;
-  }
-  __syncthreads();
-  // pass 2: blockoff (exclusive scan over blocks) and the padding rows
   for (int e = wave; e < E; e += nw) {
     int base = off[e] * tile;
     for (int b0 = 0; b0 < blocks; b0 += 64) {
       const int b = b0 + lane;
-      const int c = b < blocks ? blockcount[b * E + e] : 0;
+      const int c = b < blocks ? (staged ? bc[b * E + e] : blockcount[b * E + e]) : 0;
       const int incl = k3_wave_incl_scan(c);
-      if (b < blocks) blockoff[b * E + e] = base + incl - c;
-      base += __shfl(incl, 63, 64);
+      if (b < blocks) {
+        if (staged) bc[b * E + e] = base + incl - c;  // column e is this wave's alone
+        else blockoff[b * E + e] = base + incl - c;
+      }
+      base += __builtin_amdgcn_readlane(incl, 63);
     }
-    for (int r = off[e] * tile + count[e] + lane; r < off[e + 1] * tile; r += 64) route_map[r] = 0;
+    const int lim = off[e] * tile + count[e];
+    for (int r = lim + lane; r < off[e + 1] * tile; r += 64) route_map[r] = 0;
+    for (int i = off[e] + lane; i < off[e + 1]; i += 64) {
+      cta_batch[i] = e;
+      cta_limit[i] = min((i + 1) * tile, lim);
+    }
   }
-  // CTA tables
-  for (int i = threadIdx.x; i < off[E]; i += blockDim.x) {
-    int j = 0;
-    while (off[j + 1] <= i) ++j;
-    cta_batch[i] = j;
-    const int lim = off[j] * tile + count[j];
-    cta_limit[i] = min((i + 1) * tile, lim);
+  if (staged) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += blockDim.x) blockoff[i] = bc[i];
   }
 }
 
-// Peers of this lane among the active lanes of the wave holding the same value
-// (a ballot loop over the distinct values present).
-K3_DEV uint64_t k3_match_any(int v) {
-  uint64_t todo = __ballot(1), mine = 0;
-  while (todo) {
-    const int leader = __builtin_ctzll(todo);
-    const int lv = __shfl(v, leader, 64);
-    const uint64_t m = __ballot(v == lv) & todo;
-    if (v == lv) mine = m;
-    todo &= ~m;
+// Lanes of the wave holding the same local expert e (0 <= e < 64) as this lane:
+// the lanes with e >= 0, narrowed by one ballot per bit of e.  Meaningless for
+// lanes with e < 0.
+K3_DEV uint64_t k3_expert_peers(int e) {
+  uint64_t m = __ballot(e >= 0);
+#pragma unroll
+  for (int b = 0; b < 6; ++b) {
+    const bool bit = (e >> b) & 1;
+    const uint64_t ones = __ballot(bit);
+    m &= bit ? ones : ~ones;
   }
-  return mine;
+  return m;
 }
 
 // Route scatter (k3_moe_prefill_v4.cu:205-252).  For the expanded id
 // idx = t TOPK + k of routing block b with local expert e, the permuted row is
 // blockoff[b][e] + #{idx' < idx in block b with expert e}: a stable counting
 // sort of the block's ids by local expert.  The block's ROUTE_IDS ids are cut
-// into 64-id chunks in idx order; a chunk's per-expert counts go to LDS, one
-// scan per expert over the chunks gives each chunk's base, and a lane adds its
-// rank among the chunk's lanes of the same expert.
+// into 64-id chunks in idx order; a lane's rank among the chunk's lanes of its
+// expert comes from bit ballots, the chunk's per-expert counts go to LDS, and one
+// DPP scan per expert across the chunks (lane = chunk) turns them into each
+// chunk's base.  LDS rows are padded to MAX_E + 1 so that scan reads one bank
+// per lane.
+static_assert(MAX_E <= 64, "expert ids are matched with 6 bit ballots");
+
 extern "C" __global__ void __launch_bounds__(32 * SCATTER_WARPS) kern_k3_moe_route_scatter(
     const int* __restrict__ ids, const int* __restrict__ blockoff, int T, int rank, int E,
     int* __restrict__ route_map, int* __restrict__ exp2perm) {
-  __shared__ int hist[ROUTE_CHUNKS][MAX_E];
+  __shared__ int hist[ROUTE_CHUNKS][MAX_E + 1];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
   constexpr int CPW = (ROUTE_CHUNKS + (32 * SCATTER_WARPS / 64) - 1) / (32 * SCATTER_WARPS / 64);
   const long long base = (long long)blockIdx.x * ROUTE_IDS;
   const long long nid = (long long)T * TOPK;
-  for (int i = threadIdx.x; i < ROUTE_CHUNKS * MAX_E; i += blockDim.x) hist[i / MAX_E][i % MAX_E] = 0;
+  for (int i = threadIdx.x; i < ROUTE_CHUNKS * (MAX_E + 1); i += blockDim.x) (&hist[0][0])[i] = 0;
+  int ex[CPW];
+  long long idx[CPW];
+#pragma unroll
+  for (int r = 0; r < CPW; ++r) {
+    const int c = wave + r * nw;
+    idx[r] = base + c * 64 + lane;
+    ex[r] = c < ROUTE_CHUNKS && idx[r] < nid ? k3_local_expert(ids[idx[r]], rank, E) : -1;
+  }
   __syncthreads();
-  int ex[CPW], rk[CPW];
+  int rk[CPW];
   const uint64_t below = (1ull << lane) - 1ull;
 #pragma unroll
   for (int r = 0; r < CPW; ++r) {
     const int c = wave + r * nw;
-    ex[r] = -1;
-    rk[r] = 0;
-    if (c < ROUTE_CHUNKS) {
-      const long long idx = base + c * 64 + lane;
-      const int e = idx < nid ? k3_local_expert(ids[idx], rank, E) : -1;
-      const uint64_t peers = k3_match_any(e);
-      ex[r] = e;
-      rk[r] = __builtin_popcountll(peers & below);
-      if (e >= 0 && rk[r] == 0) hist[c][e] = __builtin_popcountll(peers);
-    }
+    const uint64_t peers = k3_expert_peers(ex[r]);
+    rk[r] = __builtin_popcountll(peers & below);
+    if (c < ROUTE_CHUNKS && ex[r] >= 0 && rk[r] == 0) hist[c][ex[r]] = __builtin_popcountll(peers);
   }
   __syncthreads();
-  if ((int)threadIdx.x < E) {
-    int run = 0;
-    for (int c = 0; c < ROUTE_CHUNKS; ++c) {
-      const int n = hist[c][threadIdx.x];
-      hist[c][threadIdx.x] = run;
-      run += n;
+  for (int e = wave; e < E; e += nw) {
+    int carry = 0;
+    for (int c0 = 0; c0 < ROUTE_CHUNKS; c0 += 64) {
+      const int c = c0 + lane;
+      const int n = c < ROUTE_CHUNKS ? hist[c][e] : 0;
+      const int incl = k3_wave_incl_scan(n);
+      if (c < ROUTE_CHUNKS) hist[c][e] = carry + incl - n;
+      carry += __builtin_amdgcn_readlane(incl, 63);
     }
   }
   __syncthreads();
 #pragma unroll
   for (int r = 0; r < CPW; ++r) {
     const int c = wave + r * nw;
-    if (c >= ROUTE_CHUNKS) continue;
-    const long long idx = base + c * 64 + lane;
-    if (idx >= nid) continue;
+    if (c >= ROUTE_CHUNKS || idx[r] >= nid) continue;
     const int e = ex[r];
-    if (e < 0) { exp2perm[idx] = -1; continue; }
+    if (e < 0) { exp2perm[idx[r]] = -1; continue; }
     const int row = blockoff[blockIdx.x * E + e] + hist[c][e] + rk[r];
-    route_map[row] = (int)(idx / TOPK);
-    exp2perm[idx] = row;
+    route_map[row] = (int)(idx[r] / TOPK);
+    exp2perm[idx[r]] = row;
   }
 }
 

@@ -96,7 +96,8 @@ def _gpu_route(ctx, ids, T, topk):
     return dict(bc=bc, bo=bo, cb=cb, cl=cl, nne=nne, tp=tp, rmap=rmap, e2p=e2p)
 
 
-@pytest.mark.parametrize("T,topk", [(16384, 8), (16384, 16), (300, 16), (257, 8)])
+# T = 40000: 157 blocks x 56 experts exceed the 8192 counts route_tables stages in LDS
+@pytest.mark.parametrize("T,topk", [(16384, 8), (16384, 16), (300, 16), (257, 8), (40000, 8)])
 def test_ep_routing_tables(ctx, T, topk):
     _case(f"routing T={T} topk={topk}")
     S, bias, rs = _router_inputs(T, 1500 + T + topk)
