@@ -18,6 +18,10 @@
 // row (k3_residual_v2.cu:229-242), so the CPU checker can replay it exactly.
 // rsqrt is 1 / sqrt with both operations correctly rounded; the softmax uses
 // the deterministic k3_expf.  Both therefore have an exact CPU counterpart.
+//
+// Rows that are read or written once (partial, prefix, prefix2, normed) move
+// with non-temporal loads and stores; gamma, sw and the candidate rows (read
+// in both passes of the mix) stay cacheable.
 #pragma once
 #include "../common/k3_dev.h"
 
@@ -202,7 +206,7 @@ K3_DEV void k3_attnres_rms_row(const uint16_t* __restrict__ blk_row, k3_u4* pv,
   k3_u4 nv[K3_KVPT];
   k3_rms_apply(pv, gamma, r, nv, t);
 #pragma unroll
-  for (int v = 0; v < K3_KVPT; ++v) k3_st16(normed_row + k3_vec_off(t, v), nv[v]);
+  for (int v = 0; v < K3_KVPT; ++v) k3_st16_nt(normed_row + k3_vec_off(t, v), nv[v]);
 }
 
 // K1b landing: prefix2 = snapshot ? bf16(pf) : bf16(f32(prefix) + f32(bf16(pf))).
@@ -215,10 +219,10 @@ typedef float k3_land_t;
 
 K3_DEV k3_u4 k3_load_land(const k3_land_t* __restrict__ partial, size_t off) {
 #ifdef LAND_BF16
-  return k3_ld16(partial + off);
+  return k3_ld16_nt(partial + off);
 #else
-  const float4 a = *(const float4*)(partial + off);
-  const float4 c = *(const float4*)(partial + off + 4);
+  const float4 a = k3_ld16f_nt(partial + off);
+  const float4 c = k3_ld16f_nt(partial + off + 4);
   k3_u4 w;
   w[0] = k3_pack_bf2(a.x, a.y);
   w[1] = k3_pack_bf2(a.z, a.w);
@@ -254,8 +258,8 @@ K3_DEV void k3_land_add_attnres_rms_body(const k3_land_t* __restrict__ partial,
   for (int v = 0; v < K3_KVPT; ++v) {
     const size_t off = (size_t)b * K3_H + k3_vec_off(t, v);
     const k3_u4 l = k3_load_land(partial, off);
-    pv[v] = snapshot ? l : k3_add_land(k3_ld16(prefix + off), l);
-    k3_st16(prefix2 + off, pv[v]);
+    pv[v] = snapshot ? l : k3_add_land(k3_ld16_nt(prefix + off), l);
+    k3_st16_nt(prefix2 + off, pv[v]);
   }
   k3_attnres_rms_row<NBC>(blocks + (size_t)b * K3_NB_MAX * K3_H, pv, sw, gamma,
                           normed + (size_t)b * K3_H, nb, K3_EPS, t);

@@ -24,11 +24,11 @@ extern "C" __global__ void __launch_bounds__(K3_RES_THREADS) kern_k3_attnres_rms
   if (nb < 0 || nb > K3_NB_MAX) return;
   k3_u4 pv[K3_KVPT];
 #pragma unroll
-  for (int v = 0; v < K3_KVPT; ++v) pv[v] = k3_ld16(prefix + (size_t)b * K3_H + k3_vec_off(t, v));
+  for (int v = 0; v < K3_KVPT; ++v) pv[v] = k3_ld16_nt(prefix + (size_t)b * K3_H + k3_vec_off(t, v));
   if (snapshot && nb < K3_NB_MAX) {
 #pragma unroll
     for (int v = 0; v < K3_KVPT; ++v)
-      k3_st16(blocks + ((size_t)b * K3_NB_MAX + nb) * K3_H + k3_vec_off(t, v), pv[v]);
+      k3_st16_nt(blocks + ((size_t)b * K3_NB_MAX + nb) * K3_H + k3_vec_off(t, v), pv[v]);
   }
   k3_attnres_rms_row<-1>(blocks + (size_t)b * K3_NB_MAX * K3_H, pv, sw, gamma,
                          normed + (size_t)b * K3_H, nb, K3_EPS, t);
@@ -56,17 +56,17 @@ extern "C" __global__ void __launch_bounds__(K3_RES_THREADS) kern_k3_land_add2(
 #pragma unroll
   for (int v = 0; v < K3_KVPT; ++v) {
     const size_t off = (size_t)b * K3_H + k3_vec_off(t, v);
-    const float4 a1 = *(const float4*)(p1 + off);
-    const float4 b1 = *(const float4*)(p1 + off + 4);
+    const float4 a1 = k3_ld16f_nt(p1 + off);
+    const float4 b1 = k3_ld16f_nt(p1 + off + 4);
     const float f1[8] = {a1.x, a1.y, a1.z, a1.w, b1.x, b1.y, b1.z, b1.w};
     float f2[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     if (two) {
-      const float4 a2 = *(const float4*)(p2 + off);
-      const float4 b2 = *(const float4*)(p2 + off + 4);
+      const float4 a2 = k3_ld16f_nt(p2 + off);
+      const float4 b2 = k3_ld16f_nt(p2 + off + 4);
       f2[0] = a2.x; f2[1] = a2.y; f2[2] = a2.z; f2[3] = a2.w;
       f2[4] = b2.x; f2[5] = b2.y; f2[6] = b2.z; f2[7] = b2.w;
     }
-    const k3_u4 pr = k3_ld16(prefix2 + off);
+    const k3_u4 pr = k3_ld16_nt(prefix2 + off);
     k3_u4 o;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -78,6 +78,6 @@ extern "C" __global__ void __launch_bounds__(K3_RES_THREADS) kern_k3_land_add2(
       }
       o[j] = k3_pack_bf2(x, y);
     }
-    k3_st16(hidden + off, o);
+    k3_st16_nt(hidden + off, o);
   }
 }
