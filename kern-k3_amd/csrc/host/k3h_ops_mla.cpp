@@ -1,5 +1,6 @@
 // Typed wrappers: MLA prep (manifest op mla_prep, k3-tp4-prefill-16k.json:404677:
-// head launch grid ceil(B/4) x 512 then gate launch grid ceil(B/4) x 384) and the
+// head launch grid ceil(B/4) x 512 then gate launch grid ceil(B/4) x 384; the
+// typed call runs both in the one launch k3h_mla_prep_fused) and the
 // latent-norm + RoPE + q packing op (module k3h_mla_rope, grid ceil(T/4) x 256).
 #include "k3h_internal.h"
 
@@ -18,14 +19,11 @@ K3H_API int k3h_mla_prep(k3h_ctx_t ctx, void* stream, int bf16_partial, const vo
     return K3H_EINVAL;
   const char* key = bf16_partial ? "k3_mla_prep_bf16+INNER=3072+MLA_FUSED=5184"
                                  : "k3_mla_prep_v2+INNER=3072+MLA_FUSED=5184";
+  // head and gate in one launch (the manifest's two entries stay in the module)
   K3hArgs h;
   h.ptr(partial).ptr(gamma_q_a).ptr(gamma_kv_a).ptr(slot_mapping).ptr(slab).i64(layer_off);
-  h.i64(page_stride).ptr(q_norm).i32(B);
-  int r = k3h_run(ctx, key, "kern_k3_mla_prep_head", k3h_cdiv(B, 4), 1, 1, 512, stream, h);
-  if (r != K3H_OK) return r;
-  K3hArgs g;
-  g.ptr(partial).ptr(mla_gate).i32(B);
-  return k3h_run(ctx, key, "kern_k3_mla_prep_gate", k3h_cdiv(B, 4), 1, 1, 384, stream, g);
+  h.i64(page_stride).ptr(q_norm).ptr(mla_gate).i32(B);
+  return k3h_run(ctx, key, "k3h_mla_prep_fused", k3h_cdiv(B, 4), 1, 1, 512, stream, h);
 }
 
 K3H_API int k3h_mla_rope_pack(k3h_ctx_t ctx, void* stream, const void* latent,

@@ -4,6 +4,8 @@
 //   kern_k3_mla_prep_head(partial, gamma_q_a, gamma_kv_a, slot_mapping, slab, layer_off,
 //                         page_stride, q_norm, B)          grid ceil(B/4), block 512
 //   kern_k3_mla_prep_gate(partial, mla_gate, B)            grid ceil(B/4), block 384
+//   k3h_mla_prep_fused(partial, gamma_q_a, gamma_kv_a, slot_mapping, slab, layer_off,
+//                      page_stride, q_norm, mla_gate, B)   grid ceil(B/4), block 512
 //
 // Entries, parameters and geometry are the reference's (k3_mla_prep_v2.cu:91,130;
 // k3_mla_prep_bf16.cu:73,112; manifest op mla_prep, k3-tp4-prefill-16k.json:404677,
@@ -40,6 +42,7 @@
 #define PG_COLS (INNER / PG_THREADS)
 #define PH_ROWS 4
 #define PH_THREADS (PH_ROWS * 128)
+static_assert(INNER % 1024 == 0, "gate columns: whole 16-byte vectors per thread of a row slice");
 #ifndef MLA_NT
 #define MLA_NT 1  // partial rows are read once: non-temporal loads
 #endif
@@ -108,11 +111,17 @@ extern "C" __global__ void __launch_bounds__(PG_THREADS) kern_k3_mla_prep_gate(
     if (r0 + r < B) k3_st16_nt(mla_gate + (size_t)(r0 + r) * INNER + c, o[r]);
 }
 
-extern "C" __global__ void __launch_bounds__(PH_THREADS) kern_k3_mla_prep_head(
-    const k3_mla_t* __restrict__ partial, const uint16_t* __restrict__ gamma_q_a,
-    const uint16_t* __restrict__ gamma_kv_a, const long long* __restrict__ slot_mapping,
-    uint16_t* __restrict__ slab, long long layer_off, long long page_stride,
-    uint16_t* __restrict__ q_norm, int B) {
+// One row per 128-thread slice (4 rows per 512-thread workgroup).  With
+// GATE the slice also lands its row's gate columns: those loads are issued
+// first and their stores do not wait for the norms.
+template <bool GATE>
+K3_DEV void k3_mla_head_rows(const k3_mla_t* __restrict__ partial,
+                             const uint16_t* __restrict__ gamma_q_a,
+                             const uint16_t* __restrict__ gamma_kv_a,
+                             const long long* __restrict__ slot_mapping,
+                             uint16_t* __restrict__ slab, long long layer_off,
+                             long long page_stride, uint16_t* __restrict__ q_norm,
+                             uint16_t* __restrict__ mla_gate, int B) {
   __shared__ float red_q[PH_ROWS][12];
   __shared__ float red_k[PH_ROWS][4];
   const int row = threadIdx.x / 128;
@@ -122,10 +131,32 @@ extern "C" __global__ void __launch_bounds__(PH_THREADS) kern_k3_mla_prep_head(
   const bool live = b < B;
   const k3_mla_t* __restrict__ P = partial + (size_t)(live ? b : 0) * MLA_FUSED;
 
+  constexpr int GV = INNER / 8 / 128;  // gate vectors (8 values) per thread
+  k3_u4 gv[GATE ? GV : 1];
+  if (GATE) {
+#pragma unroll
+    for (int k = 0; k < GV; ++k) {
+      const k3_mla_t* src = P + HEADC + 8 * ((threadIdx.x & 127) + 128 * k);
+#ifdef K3_MLA_BF16
+      gv[k] = k3_ld16_nt(src);
+#else
+      const k3_u4 x = k3_ld16_nt(src), y = k3_ld16_nt(src + 4);
+      gv[k][0] = k3_pack_bf2(__uint_as_float(x[0]), __uint_as_float(x[1]));
+      gv[k][1] = k3_pack_bf2(__uint_as_float(x[2]), __uint_as_float(x[3]));
+      gv[k][2] = k3_pack_bf2(__uint_as_float(y[0]), __uint_as_float(y[1]));
+      gv[k][3] = k3_pack_bf2(__uint_as_float(y[2]), __uint_as_float(y[3]));
+#endif
+    }
+  }
   float4 qv[3];
 #pragma unroll
   for (int k = 0; k < 3; ++k) qv[k] = k3_mla_ld4(P + 4 * (32 * (3 * sub + k) + lane));
   const float4 kv = k3_mla_ld4(P + 4 * (QU + 32 * sub + lane));
+  if (GATE && live) {
+#pragma unroll
+    for (int k = 0; k < GV; ++k)
+      k3_st16_nt(mla_gate + (size_t)b * INNER + 8 * ((threadIdx.x & 127) + 128 * k), gv[k]);
+  }
 #pragma unroll
   for (int k = 0; k < 3; ++k) {
     const float p = k3_sum32(k3_unit_sq(qv[k]));
@@ -166,4 +197,24 @@ extern "C" __global__ void __launch_bounds__(PH_THREADS) kern_k3_mla_prep_head(
     o[1] = k3_pack_bf2(v.z, v.w);
     *(k3_u2*)(rowp + KV_LORA + 4 * lane) = o;
   }
+}
+
+extern "C" __global__ void __launch_bounds__(PH_THREADS) kern_k3_mla_prep_head(
+    const k3_mla_t* __restrict__ partial, const uint16_t* __restrict__ gamma_q_a,
+    const uint16_t* __restrict__ gamma_kv_a, const long long* __restrict__ slot_mapping,
+    uint16_t* __restrict__ slab, long long layer_off, long long page_stride,
+    uint16_t* __restrict__ q_norm, int B) {
+  k3_mla_head_rows<false>(partial, gamma_q_a, gamma_kv_a, slot_mapping, slab, layer_off,
+                          page_stride, q_norm, nullptr, B);
+}
+
+// Both halves in one launch (no reference counterpart: the reference launches
+// head and gate separately): grid ceil(B / 4), block 512.
+extern "C" __global__ void __launch_bounds__(PH_THREADS) k3h_mla_prep_fused(
+    const k3_mla_t* __restrict__ partial, const uint16_t* __restrict__ gamma_q_a,
+    const uint16_t* __restrict__ gamma_kv_a, const long long* __restrict__ slot_mapping,
+    uint16_t* __restrict__ slab, long long layer_off, long long page_stride,
+    uint16_t* __restrict__ q_norm, uint16_t* __restrict__ mla_gate, int B) {
+  k3_mla_head_rows<true>(partial, gamma_q_a, gamma_kv_a, slot_mapping, slab, layer_off,
+                         page_stride, q_norm, mla_gate, B);
 }
