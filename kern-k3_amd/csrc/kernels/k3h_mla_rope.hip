@@ -92,9 +92,17 @@ extern "C" __global__ void __launch_bounds__(256) k3h_mla_rope_pack(
   const int nvec = H * (K3_QH / 8);
   const uint16_t* qrow = q + (size_t)t * H * K3_QH;
   uint16_t* orow = q_out + (size_t)t * H * K3_QH;
-  for (int w = l; w < nvec; w += 64) {
-    const int v = w % (K3_QH / 8);
-    const k3_u4 a = k3_ld16_nt(qrow + 8 * w);
-    k3_st16_nt(orow + 8 * w, v < 16 ? a : k3_rope_vec(a, cs, 4 * (v - 16)));
+  // batches of 8 vectors per lane, all loaded before the first store (indices
+  // past the row are clamped for the load and skipped for the store)
+  for (int w0 = 0; w0 < nvec; w0 += 64 * 8) {
+    k3_u4 a[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) a[k] = k3_ld16_nt(qrow + 8 * min(w0 + l + 64 * k, nvec - 1));
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int w = w0 + l + 64 * k;
+      const int v = w % (K3_QH / 8);
+      if (w < nvec) k3_st16_nt(orow + 8 * w, v < 16 ? a[k] : k3_rope_vec(a[k], cs, 4 * (v - 16)));
+    }
   }
 }
