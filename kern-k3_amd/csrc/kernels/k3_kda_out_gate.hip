@@ -26,23 +26,9 @@
 #define K11_RMS_EPS 1e-5f
 static_assert(HEADS % 8 == 0, "HEADS must be a multiple of 8");
 
-extern "C" __global__ void __launch_bounds__(128) kern_k3_kda_out_gate(
-    const uint16_t* __restrict__ attn, const uint16_t* __restrict__ gate_partial,
-    const float* __restrict__ gamma_o, uint16_t* __restrict__ gated,
-    const int* __restrict__ span_at, int span) {
-  const int i = blockIdx.x;
-  if (i >= span) return;
-  const int h = blockIdx.y * 8 + threadIdx.x / 16;
-  const int d0 = (threadIdx.x % 16) * 8;
-  const size_t col = (size_t)h * 128 + d0;
-  const int b = span_at[0] + i;
-
-  const k3_u4 av = k3_ld16_nt(attn + (size_t)i * K11_INNER + col);
-  const k3_u4 gv = k3_ld16_nt(gate_partial + (size_t)b * K11_KDA_FUSED + 3 * K11_INNER + col);
-  const float4 gm0 = *(const float4*)(gamma_o + d0);
-  const float4 gm1 = *(const float4*)(gamma_o + d0 + 4);
-  const float gm[8] = {gm0.x, gm0.y, gm0.z, gm0.w, gm1.x, gm1.y, gm1.z, gm1.w};
-
+// One (row, 16-byte column vector) of the gate: the per-head sum of squares
+// runs over the 16 lanes of the head (a 16-lane row of the wave).
+K3_DEV k3_u4 k11_gate_vec(k3_u4 av, k3_u4 gv, const float* gm) {
   float a[8];
 #pragma unroll
   for (int k = 0; k < 4; ++k) { a[2 * k] = k3_bf_lo(av[k]); a[2 * k + 1] = k3_bf_hi(av[k]); }
@@ -51,7 +37,6 @@ extern "C" __global__ void __launch_bounds__(128) kern_k3_kda_out_gate(
   for (int k = 0; k < 8; ++k) ss = __builtin_fmaf(a[k], a[k], ss);
   ss = k3_sum16(ss);
   const float r = k3_rsqrt_cr(__builtin_fmaf(ss, 1.0f / 128.0f, K11_RMS_EPS));
-
   k3_u4 out;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
@@ -61,5 +46,29 @@ extern "C" __global__ void __launch_bounds__(128) kern_k3_kda_out_gate(
     const float t1 = k3_land(k3_sigmoid_fast(k3_bf_hi(gv[k])));
     out[k] = k3_pack_bf2(o0 * t0, o1 * t1);
   }
-  k3_st16_nt(gated + (size_t)b * K11_INNER + col, out);
+  return out;
+}
+
+// Tiles are taken in memory order: linear workgroup id L (x fastest) is span row
+// L / gridDim.y, column block L % gridDim.y, so neighbouring workgroups read
+// neighbouring 1 KB pieces of one row instead of one piece from each of
+// consecutive rows.  Same grid, same tiles, same per-element work.
+extern "C" __global__ void __launch_bounds__(128) kern_k3_kda_out_gate(
+    const uint16_t* __restrict__ attn, const uint16_t* __restrict__ gate_partial,
+    const float* __restrict__ gamma_o, uint16_t* __restrict__ gated,
+    const int* __restrict__ span_at, int span) {
+  const uint32_t L = blockIdx.x + gridDim.x * blockIdx.y;
+  const int i = (int)(L / gridDim.y);
+  if (i >= span) return;
+  const int h = (int)(L % gridDim.y) * 8 + threadIdx.x / 16;
+  const int d0 = (threadIdx.x % 16) * 8;
+  const size_t col = (size_t)h * 128 + d0;
+  const int b = span_at[0] + i;
+
+  const k3_u4 av = k3_ld16_nt(attn + (size_t)i * K11_INNER + col);
+  const k3_u4 gv = k3_ld16_nt(gate_partial + (size_t)b * K11_KDA_FUSED + 3 * K11_INNER + col);
+  const float4 gm0 = *(const float4*)(gamma_o + d0);
+  const float4 gm1 = *(const float4*)(gamma_o + d0 + 4);
+  const float gm[8] = {gm0.x, gm0.y, gm0.z, gm0.w, gm1.x, gm1.y, gm1.z, gm1.w};
+  k3_st16_nt(gated + (size_t)b * K11_INNER + col, k11_gate_vec(av, gv, gm));
 }
