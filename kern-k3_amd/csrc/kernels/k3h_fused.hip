@@ -22,18 +22,25 @@
 // at the same v.  Two rows per workgroup streams at the rate of a plain
 // two-read / 1.5-write copy on MI355X, where one row per 128-thread workgroup
 // loses about 4%.  The E8M0 bytes of four quads are gathered into one lane and
-// stored as a word.  A half whose row is past B still takes part in the
-// workgroup barrier but loads and stores nothing.
+// stored as a word, after the quantisation loop.  A half whose row is past B
+// still takes part in the workgroup barrier but stores nothing.
+//
+// Wait discipline: the vector memory counter counts stores as well as loads,
+// in issue order, so waiting for a load also waits for every store issued
+// before it.  gamma is therefore loaded one vector ahead of its use (the load
+// for v + 1 goes out before the stores of v), and the quantisation loop has no
+// branch (normed is a template parameter, the E8M0 words leave after the
+// loop), which lets the compiler wait for exactly the load it needs.
 #include "k3_residual_row.h"
 #include "k3_mx.h"
 
 #define K3_FUSED_ROWS 2
 
-extern "C" __global__ void __launch_bounds__(K3_RES_THREADS * K3_FUSED_ROWS) k3h_residual_rms_mxfp8(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ residual,
-    const uint16_t* __restrict__ gamma, uint16_t* __restrict__ residual_out,
-    uint8_t* __restrict__ q, uint8_t* __restrict__ sf, uint16_t* __restrict__ normed,
-    float eps, int B) {
+template <bool NORMED>
+K3_DEV void k3h_fused_rows(const uint16_t* __restrict__ x, const uint16_t* __restrict__ residual,
+                           const uint16_t* __restrict__ gamma, uint16_t* __restrict__ residual_out,
+                           uint8_t* __restrict__ q, uint8_t* __restrict__ sf, uint16_t* __restrict__ normed,
+                           float eps, int B) {
   __shared__ float s_red[K3_FUSED_ROWS * K3_NHW];
   const int half = threadIdx.x / K3_RES_THREADS;
   const int t = threadIdx.x % K3_RES_THREADS;
@@ -44,12 +51,17 @@ extern "C" __global__ void __launch_bounds__(K3_RES_THREADS * K3_FUSED_ROWS) k3h
   // Loads are unconditional (a dead half reads row 0, which exists because the
   // grid only covers B >= 1): a predicated load would be compiled as a branch
   // with a full wait per vector and lose the memory-level parallelism.
-  k3_u4 pv[K3_KVPT];
+  k3_u4 rv[K3_KVPT], xv[K3_KVPT];
 #pragma unroll
   for (int v = 0; v < K3_KVPT; ++v) {
     const size_t off = row + k3_vec_off(t, v);
-    pv[v] = k3_add_land(k3_ld16_nt(residual + off), k3_ld16_nt(x + off));
+    rv[v] = k3_ld16_nt(residual + off);
+    xv[v] = k3_ld16_nt(x + off);
   }
+  k3_u4 gnext = k3_ld16(gamma + k3_vec_off(t, 0));
+  k3_u4 pv[K3_KVPT];
+#pragma unroll
+  for (int v = 0; v < K3_KVPT; ++v) pv[v] = k3_add_land(rv[v], xv[v]);
   if (live) {
 #pragma unroll
     for (int v = 0; v < K3_KVPT; ++v) k3_st16_nt(residual_out + row + k3_vec_off(t, v), pv[v]);
@@ -58,10 +70,12 @@ extern "C" __global__ void __launch_bounds__(K3_RES_THREADS * K3_FUSED_ROWS) k3h
   const float tot = k3_block_sum128(k3_row_sumsq(pv), s_red + half * K3_NHW, t);
   if (!live) return;  // no barrier follows
   const float r = k3_row_rscale(tot, eps);
+  uint32_t sfw[K3_KVPT];
 #pragma unroll
   for (int v = 0; v < K3_KVPT; ++v) {
     const int u = k3_vec_off(t, v);
-    const k3_u4 g = k3_ld16(gamma + u);
+    const k3_u4 g = gnext;
+    if (v + 1 < K3_KVPT) gnext = k3_ld16(gamma + k3_vec_off(t, v + 1));
     k3_u4 nv;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -70,11 +84,24 @@ extern "C" __global__ void __launch_bounds__(K3_RES_THREADS * K3_FUSED_ROWS) k3h
     const uint32_t sfb = (uint32_t)(k3_mx_quad(nv, &qv) + 127);
     k3_st8_nt(q + row + u, qv);
     // lane 16m gathers the bytes of quads 4m .. 4m + 3 (lanes 16m + 4k)
-    const uint32_t w = sfb | (k3_swz_xor_u32<4>(sfb) << 8) | (k3_swz_xor_u32<8>(sfb) << 16) |
-                       (k3_swz_xor_u32<12>(sfb) << 24);
-    if ((t & 15) == 0) *(uint32_t*)(sf + (size_t)b * (K3_H / 32) + (u >> 5)) = w;
-    if (normed) k3_st16(normed + row + u, nv);
+    sfw[v] = sfb | (k3_swz_xor_u32<4>(sfb) << 8) | (k3_swz_xor_u32<8>(sfb) << 16) |
+             (k3_swz_xor_u32<12>(sfb) << 24);
+    if (NORMED) k3_st16(normed + row + u, nv);
   }
+  if ((t & 15) == 0) {
+#pragma unroll
+    for (int v = 0; v < K3_KVPT; ++v)
+      *(uint32_t*)(sf + (size_t)b * (K3_H / 32) + (k3_vec_off(t, v) >> 5)) = sfw[v];
+  }
+}
+
+extern "C" __global__ void __launch_bounds__(K3_RES_THREADS * K3_FUSED_ROWS) k3h_residual_rms_mxfp8(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ residual,
+    const uint16_t* __restrict__ gamma, uint16_t* __restrict__ residual_out,
+    uint8_t* __restrict__ q, uint8_t* __restrict__ sf, uint16_t* __restrict__ normed,
+    float eps, int B) {
+  if (normed) k3h_fused_rows<true>(x, residual, gamma, residual_out, q, sf, normed, eps, B);
+  else k3h_fused_rows<false>(x, residual, gamma, residual_out, q, sf, normed, eps, B);
 }
 
 // Plain 16-byte streaming copy (measurement support: the HBM ceiling and the
