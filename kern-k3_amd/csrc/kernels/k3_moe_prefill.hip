@@ -272,24 +272,124 @@ extern "C" __global__ void __launch_bounds__(32 * SCATTER_WARPS) kern_k3_moe_rou
 // ascending of wts[t][k] * f32(fc2[exp2perm[t TOPK + k], c])) over the local
 // slots, f32 accumulator from 0, one fma per term.  Manifest geometry: grid
 // ceil(T / 2), block 128, so each wave owns one token: lanes < TOPK read the
-// token's slots and a ballot compacts the local ones (k ascending).  The row is
-// walked FV 16-byte vectors per lane at a time; the loads of up to four slots x
-// FV vectors are issued before their fmas, which then run in slot order.
-#ifndef FV
-#define FV 4
-#endif
-#ifndef FS
-#define FS 8
-#endif
+// token's slots and a ballot compacts the local ones (k ascending).
+//
+// The row is walked in steps of FVN 16-byte vectors per lane.  The number of
+// local slots n is uniform over the wave, so the step loop is instantiated per
+// n (k3_fin_row<n, FVN>) and contains no branch: vector indices past the row
+// are clamped for loads and stores alike (a clamped lane loads, sums and
+// stores exactly the bytes of the row's last vector), and the next step's loads
+// are issued before this step's stores.  The vector memory counter counts
+// stores too, in issue order, so the compiler can then wait for each load
+// without draining the stores before it.
 #ifndef FIN_NT
 #define FIN_NT 1
 #endif
+// Vectors per lane per step, by number of local slots (n = 1, 2, 3..4, 5..8).
+// Wide steps keep 14-28 row loads of one wave in flight; the kernel then runs
+// one wave per SIMD (about 280 VGPRs), which on MI355X streams this gather
+// faster than narrower steps at two or three waves per SIMD.  7 divides the
+// 14 vectors per lane of a 7168-column row.
+#ifndef FIN_FV1
+#define FIN_FV1 7
+#endif
+#ifndef FIN_FV2
+#define FIN_FV2 7
+#endif
+#ifndef FIN_FV4
+#define FIN_FV4 4
+#endif
+#ifndef FIN_FV8
+#define FIN_FV8 2
+#endif
+
+K3_DEV k3_u4 k3_fin_ld(const uint16_t* p) { return FIN_NT ? k3_ld16_nt(p) : k3_ld16(p); }
+
+template <int NS, int FVN>
+K3_DEV void k3_fin_row(const uint16_t* __restrict__ fc2, const int* srow, const float* sw,
+                       uint16_t* __restrict__ orow, int cols, int lane) {
+  const int nvec = cols >> 3;
+  const int nsteps = (nvec + 64 * FVN - 1) / (64 * FVN);
+  k3_u4 x[NS][FVN];
+  auto vec = [&](int step, int c) { return min(step * 64 * FVN + lane + 64 * c, nvec - 1); };
+  auto load = [&](int step) {
+#pragma unroll
+    for (int i = 0; i < NS; ++i)
+#pragma unroll
+      for (int c = 0; c < FVN; ++c) x[i][c] = k3_fin_ld(fc2 + (size_t)srow[i] * cols + (size_t)vec(step, c) * 8);
+  };
+  auto sum_store = [&](int step, bool prefetch) {
+    float acc[FVN][8];
+#pragma unroll
+    for (int c = 0; c < FVN; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[c][j] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NS; ++i)
+#pragma unroll
+      for (int c = 0; c < FVN; ++c)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc[c][2 * j] = __builtin_fmaf(sw[i], k3_bf_lo(x[i][c][j]), acc[c][2 * j]);
+          acc[c][2 * j + 1] = __builtin_fmaf(sw[i], k3_bf_hi(x[i][c][j]), acc[c][2 * j + 1]);
+        }
+    if (prefetch) load(step + 1);
+#pragma unroll
+    for (int c = 0; c < FVN; ++c) {
+      k3_u4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = k3_pack_bf2(acc[c][2 * j], acc[c][2 * j + 1]);
+      k3_st16_nt(orow + (size_t)vec(step, c) * 8, o);
+    }
+  };
+  load(0);
+  if (nsteps == 1) {
+    sum_store(0, false);
+    return;
+  }
+  // Step 0 is peeled so that the loop is entered, and re-entered, with the same
+  // operations in flight (the next step's loads, then this step's stores).
+  sum_store(0, true);
+  for (int step = 1; step + 1 < nsteps; ++step) sum_store(step, true);
+  sum_store(nsteps - 1, false);
+}
+
+// More than eight local slots (TOPK 16 only): groups of eight slots per step.
+K3_DEV void k3_fin_row_many(const uint16_t* __restrict__ fc2, const int* srow, const float* sw,
+                            int n, uint16_t* __restrict__ orow, int cols, int lane) {
+  const int nvec = cols >> 3;
+  for (int v0 = 0; v0 < nvec; v0 += 64) {
+    const int v = min(v0 + lane, nvec - 1);
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+    for (int i0 = 0; i0 < n; i0 += 8) {
+      k3_u4 x[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] = k3_fin_ld(fc2 + (size_t)srow[min(i0 + i, n - 1)] * cols + (size_t)v * 8);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (i0 + i >= n) break;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc[2 * j] = __builtin_fmaf(sw[i0 + i], k3_bf_lo(x[i][j]), acc[2 * j]);
+          acc[2 * j + 1] = __builtin_fmaf(sw[i0 + i], k3_bf_hi(x[i][j]), acc[2 * j + 1]);
+        }
+      }
+    }
+    k3_u4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = k3_pack_bf2(acc[2 * j], acc[2 * j + 1]);
+    k3_st16_nt(orow + (size_t)v * 8, o);
+  }
+}
+
 extern "C" __global__ void __launch_bounds__(128) kern_k3_moe_finalize(
     const uint16_t* __restrict__ fc2, const int* __restrict__ exp2perm,
     const float* __restrict__ wts, uint16_t* __restrict__ out, int T, int cols) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 2 + (threadIdx.x >> 6);
-  if (t >= T) return;
+  if (t >= T || cols < 8) return;
   int p = -1;
   float w = 0.0f;
   if (lane < TOPK) {
@@ -310,51 +410,22 @@ extern "C" __global__ void __launch_bounds__(128) kern_k3_moe_finalize(
       m &= m - 1;
     }
   }
-  const int nvec = cols >> 3;  // 16-byte vectors per row
   uint16_t* __restrict__ orow = out + (size_t)t * cols;
-  for (int v0 = lane; v0 < nvec; v0 += 64 * FV) {
-    float acc[FV][8];
-#pragma unroll
-    for (int c = 0; c < FV; ++c)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[c][j] = 0.0f;
-#pragma unroll
-    for (int i0 = 0; i0 < TOPK; i0 += FS) {
-      if (i0 >= n) break;
-      k3_u4 x[FS][FV];
-#pragma unroll
-      for (int i = 0; i < FS; ++i)
-#pragma unroll
-        for (int c = 0; c < FV; ++c) {
-          const int v = v0 + 64 * c;
-          x[i][c] = (i0 + i < n && v < nvec)
-                        ? (FIN_NT ? k3_ld16_nt(fc2 + (size_t)srow[i0 + i] * cols + (size_t)v * 8)
-                                  : k3_ld16(fc2 + (size_t)srow[i0 + i] * cols + (size_t)v * 8))
-                        : k3_u4{0, 0, 0, 0};
-        }
-#pragma unroll
-      for (int i = 0; i < FS; ++i) {
-        if (i0 + i >= n) break;
-        const float wi = sw[i0 + i];
-#pragma unroll
-        for (int c = 0; c < FV; ++c)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            acc[c][2 * j] = __builtin_fmaf(wi, k3_bf_lo(x[i][c][j]), acc[c][2 * j]);
-            acc[c][2 * j + 1] = __builtin_fmaf(wi, k3_bf_hi(x[i][c][j]), acc[c][2 * j + 1]);
-          }
-      }
+  switch (n) {
+    case 0: {  // no local slot: the row is bf16(0)
+      const k3_u4 z = {0u, 0u, 0u, 0u};
+      for (int v = lane; v < (cols >> 3); v += 64) k3_st16_nt(orow + (size_t)v * 8, z);
+      break;
     }
-#pragma unroll
-    for (int c = 0; c < FV; ++c) {
-      const int v = v0 + 64 * c;
-      if (v < nvec) {
-        k3_u4 o;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) o[j] = k3_pack_bf2(acc[c][2 * j], acc[c][2 * j + 1]);
-        k3_st16_nt(orow + (size_t)v * 8, o);
-      }
-    }
+    case 1: k3_fin_row<1, FIN_FV1>(fc2, srow, sw, orow, cols, lane); break;
+    case 2: k3_fin_row<2, FIN_FV2>(fc2, srow, sw, orow, cols, lane); break;
+    case 3: k3_fin_row<3, FIN_FV4>(fc2, srow, sw, orow, cols, lane); break;
+    case 4: k3_fin_row<4, FIN_FV4>(fc2, srow, sw, orow, cols, lane); break;
+    case 5: k3_fin_row<5, FIN_FV8>(fc2, srow, sw, orow, cols, lane); break;
+    case 6: k3_fin_row<6, FIN_FV8>(fc2, srow, sw, orow, cols, lane); break;
+    case 7: k3_fin_row<7, FIN_FV8>(fc2, srow, sw, orow, cols, lane); break;
+    case 8: k3_fin_row<8, FIN_FV8>(fc2, srow, sw, orow, cols, lane); break;
+    default: k3_fin_row_many(fc2, srow, sw, n, orow, cols, lane); break;
   }
 }
 

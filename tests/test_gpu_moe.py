@@ -162,6 +162,26 @@ def test_finalize_cols(ctx, cols):
     _eq("finalize", from_dev(out), O.moe_finalize(fc2, from_dev(d["e2p"]), wts, T, topk, cols))
 
 
+@pytest.mark.parametrize("topk,cols", [(8, 7168), (16, 7168), (8, 1032), (16, 8)])
+def test_finalize_every_slot_count(ctx, topk, cols):
+    """Token t has exactly t % (topk + 1) local slots, at random slot positions and
+    rows: every per-count path of the finalize kernel (0 .. topk live slots), and
+    for cols = 1032 a last step that covers only part of the row."""
+    _case(f"finalize slot counts topk={topk} cols={cols}")
+    g = rng(1750 + topk + cols)
+    T, rows = 4 * (topk + 1) + 3, 97
+    e2p = np.full((T, topk), -1, dtype=np.int32)
+    for t in range(T):
+        live = g.choice(topk, size=t % (topk + 1), replace=False)
+        e2p[t, live] = g.integers(0, rows, size=live.size)
+    wts = g.random((T, topk), dtype=np.float32) * 2 - 0.5
+    fc2 = normal_bf16(g, (rows, cols))
+    out = torch.empty((T, cols), dtype=torch.bfloat16, device="cuda")
+    ctx.moe_finalize(to_dev(fc2), to_dev(e2p.reshape(-1)), to_dev(wts), out, T, cols, topk=topk)
+    torch.cuda.synchronize()
+    _eq("finalize", from_dev(out), O.moe_finalize(fc2, e2p.reshape(-1), wts, T, topk, cols))
+
+
 def test_weight_layouts(ctx):
     _case("w_shuffle / sf_shuffle")
     g = rng(1800)
