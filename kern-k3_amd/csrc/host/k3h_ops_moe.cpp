@@ -5,6 +5,7 @@
 // moe_route_tables 405046 (1, 1024), moe_route_scatter 405120 (ceil(T/256),
 // 512), moe_finalize 405686 (ceil(T/2), 128).  topk selects the code object:
 // 16 is the manifest build, 8 the "+TOPK=8" build.
+#include <algorithm>
 #include <string>
 
 #include "k3h_internal.h"
@@ -119,8 +120,10 @@ K3H_API int k3h_moe_permute_mx(k3h_ctx_t ctx, void* stream, const void* q, const
     return K3H_EINVAL;
   K3hArgs a;
   a.ptr(q).ptr(sf).ptr(route_map).ptr(total_padded).i32(max_rows).i32(cols).ptr(pq).ptr(psf);
-  // one row per wave over max_rows; rows past *total_padded exit
-  return k3h_run(ctx, kMoeV4, "k3h_moe_permute_mx", k3h_cdiv(max_rows, 4), 1, 1, 256, stream, a);
+  // one row per wave; rows past *total_padded exit, and past 64K rows (max_rows is
+  // often a capacity) the waves stride instead of launching empty workgroups
+  const uint32_t grid = std::min<uint32_t>(k3h_cdiv(max_rows, 4), 16384u);
+  return k3h_run(ctx, kMoeV4, "k3h_moe_permute_mx", grid, 1, 1, 256, stream, a);
 }
 
 K3H_API int k3h_moe_w_shuffle(k3h_ctx_t ctx, void* stream, const void* src, void* dst,

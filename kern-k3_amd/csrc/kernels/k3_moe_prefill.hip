@@ -19,7 +19,7 @@
 //
 // Plus one operator with no reference entry (module key k3_moe_prefill_v4+...):
 //   k3h_moe_permute_mx(q, sf, route_map, total_padded, max_rows, cols, pq, psf)
-//       grid ceil(max_rows / 4), block 256: pq[r] = q[route_map[r]],
+//       grid min(ceil(max_rows / 4), 16384), block 256: pq[r] = q[route_map[r]],
 //       psf[r] = sf[route_map[r]] for r < min(*total_padded, max_rows) (the
 //       reference gathers these rows inside moe_fc1).
 #include "k3_mx.h"
@@ -433,9 +433,27 @@ extern "C" __global__ void __launch_bounds__(128) kern_k3_moe_finalize(
 // expert-contiguous order of route_map (padding rows carry token 0, as routed).
 // One row per wave (r = global wave id, striding by the grid's waves), rows
 // r >= *total_padded exit; all of a row's loads are issued before its stores.
-// Per row cols payload bytes (cols / 1024 16-byte vectors per lane) and cols / 32
-// scale bytes (one word per lane).  cols % 1024 == 0, cols <= 16384.
-#define PM_MAXV 16
+// Per row cols payload bytes (NV = cols / 1024 16-byte vectors per lane, a
+// template parameter so that no load is predicated) and cols / 32 scale bytes
+// (up to two words per lane; lanes past the row's words re-read its last word
+// and do not store).  cols % 1024 == 0, cols <= 16384.
+template <int NV>
+K3_DEV void k3_permute_row(const uint8_t* __restrict__ q, const uint8_t* __restrict__ sf,
+                           int t, int r, int cols, uint8_t* __restrict__ pq,
+                           uint8_t* __restrict__ psf, int lane) {
+  const int sfw = cols >> 7;  // scale words per row: up to 128, two per lane
+  k3_u4 v[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) v[j] = k3_ld16_nt(q + (size_t)t * cols + (size_t)(lane + 64 * j) * 16);
+  const uint32_t* srow = (const uint32_t*)(sf + (size_t)t * (cols >> 5));
+  const uint32_t sw0 = srow[min(lane, sfw - 1)], sw1 = srow[min(lane + 64, sfw - 1)];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) k3_st16_nt(pq + (size_t)r * cols + (size_t)(lane + 64 * j) * 16, v[j]);
+  uint32_t* drow = (uint32_t*)(psf + (size_t)r * (cols >> 5));
+  if (lane < sfw) drow[lane] = sw0;
+  if (lane + 64 < sfw) drow[lane + 64] = sw1;
+}
+
 extern "C" __global__ void __launch_bounds__(256) k3h_moe_permute_mx(
     const uint8_t* __restrict__ q, const uint8_t* __restrict__ sf, const int* __restrict__ route_map,
     const int* __restrict__ total_padded, int max_rows, int cols, uint8_t* __restrict__ pq,
@@ -443,21 +461,18 @@ extern "C" __global__ void __launch_bounds__(256) k3h_moe_permute_mx(
   const int lane = threadIdx.x & 63;
   const int nrows = min(total_padded[0], max_rows);  // pq / psf hold max_rows rows
   const int nwaves = gridDim.x * (blockDim.x >> 6);
-  const int nv = cols >> 10;   // 16-byte vectors per lane
-  const int sfw = cols >> 7;   // scale words per row
   for (int r = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); r < nrows; r += nwaves) {
     const int t = route_map[r];
-    const uint8_t* src = q + (size_t)t * cols;
-    uint8_t* dst = pq + (size_t)r * cols;
-    k3_u4 v[PM_MAXV];
-#pragma unroll
-    for (int k = 0; k < PM_MAXV; ++k)
-      if (k < nv) v[k] = k3_ld16_nt(src + (size_t)(lane + 64 * k) * 16);
-    const uint32_t sw = lane < sfw ? *(const uint32_t*)(sf + (size_t)t * (cols >> 5) + 4 * lane) : 0u;
-#pragma unroll
-    for (int k = 0; k < PM_MAXV; ++k)
-      if (k < nv) k3_st16_nt(dst + (size_t)(lane + 64 * k) * 16, v[k]);
-    if (lane < sfw) *(uint32_t*)(psf + (size_t)r * (cols >> 5) + 4 * lane) = sw;
+    switch (cols >> 10) {
+#define K3_PM_CASE(n) \
+  case n: k3_permute_row<n>(q, sf, t, r, cols, pq, psf, lane); break;
+      K3_PM_CASE(1) K3_PM_CASE(2) K3_PM_CASE(3) K3_PM_CASE(4)
+      K3_PM_CASE(5) K3_PM_CASE(6) K3_PM_CASE(7) K3_PM_CASE(8)
+      K3_PM_CASE(9) K3_PM_CASE(10) K3_PM_CASE(11) K3_PM_CASE(12)
+      K3_PM_CASE(13) K3_PM_CASE(14) K3_PM_CASE(15) K3_PM_CASE(16)
+#undef K3_PM_CASE
+      default: break;
+    }
   }
 }
 

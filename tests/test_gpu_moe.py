@@ -147,6 +147,27 @@ def test_permute_and_finalize_config5(ctx):
     _eq("finalize", from_dev(out), want)
 
 
+# 70000 rows: past the 16384-workgroup grid cap, so waves stride over rows;
+# 16384 columns: the widest row (16 vectors per lane)
+@pytest.mark.parametrize("rows,tp,cols", [(70000, 69001, 1024), (300, 257, 16384)])
+def test_permute_rows_and_widths(ctx, rows, tp, cols):
+    _case(f"permute rows={rows} tp={tp} cols={cols}")
+    g = rng(1650 + cols)
+    T = 1000
+    q = g.integers(0, 256, (T, cols), dtype=np.uint8)
+    sf = g.integers(0, 256, (T, cols // 32), dtype=np.uint8)
+    rmap = g.integers(0, T, rows, dtype=np.int32)
+    pq = torch.zeros((rows, cols), dtype=torch.uint8, device="cuda")
+    psf = torch.zeros((rows, cols // 32), dtype=torch.uint8, device="cuda")
+    d_tp = torch.tensor([tp], dtype=torch.int32, device="cuda")
+    ctx.moe_permute_mx(to_dev(q), to_dev(sf), to_dev(rmap), d_tp, cols, pq, psf)
+    torch.cuda.synchronize()
+    wpq, wpsf = O.moe_permute_mx(q, sf, rmap, tp, cols)
+    _eq("pq", from_dev(pq)[:tp], wpq)
+    _eq("psf", from_dev(psf)[:tp], wpsf)
+    assert not from_dev(pq)[tp:].any() and not from_dev(psf)[tp:].any()  # rows past tp untouched
+
+
 @pytest.mark.parametrize("cols", [3584, 7168, 8])
 def test_finalize_cols(ctx, cols):
     T, topk = 1000, 16
