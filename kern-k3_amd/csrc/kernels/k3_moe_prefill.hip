@@ -53,18 +53,19 @@ extern "C" __global__ void __launch_bounds__(256) kern_k3_moe_quant(
   const long long nblk = (long long)rows * cols / 32;
   const int l = threadIdx.x & 63;
   const long long first = (long long)blockIdx.x * blockDim.x + (threadIdx.x & ~63);
+  if (first >= nblk) return;
   k3_u4 v[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const long long blk = first + 16 * j + (l >> 2);
-    if (blk < nblk) v[j] = k3_ld16_nt(x + blk * 32 + (l & 3) * 8);
+  for (int j = 0; j < 4; ++j) {  // past the end: the last block is re-read, nothing is stored
+    const long long blk = min(first + 16 * j + (l >> 2), nblk - 1);
+    v[j] = k3_ld16_nt(x + blk * 32 + (l & 3) * 8);
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const long long blk = first + 16 * j + (l >> 2);
-    if (blk < nblk) {  // uniform over the quad that shares the block
-      k3_u2 qv;
-      const int e = k3_mx_quad(v[j], &qv);
+    k3_u2 qv;
+    const int e = k3_mx_quad(v[j], &qv);  // quad-wide: every lane takes part
+    if (blk < nblk) {
       k3_st8_nt(q + blk * 32 + (l & 3) * 8, qv);
       if ((l & 3) == 0) sf[blk] = (uint8_t)(e + 127);
     }
