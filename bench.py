@@ -84,7 +84,8 @@ def cpu_baseline(x, res, gamma, gpu_out, budget_s: float = 10.0) -> dict:
         "cores": O.num_threads(),
         "kind": "port",
         "sample": f"full {rows}x{H} workload, median of {len(times)} oracle passes "
-                  f"({best * 1e3:.0f} ms each); bit-exact vs GPU: {match}",
+                  f"({best * 1e3:.0f} ms each) on {O.num_threads()} OpenMP threads of "
+                  f"{os.cpu_count()} hardware threads; bit-exact vs GPU: {match}",
     }
 
 
@@ -111,8 +112,9 @@ def copy_ceiling(ctx, rows: int, reps: int) -> float:
 
 
 def bench_ops(ctx, reps: int, out_path: str | None) -> list:
-    """Every op at its BASELINE config shape: per-launch HIP events with a 512 MB
-    cache-flush write between launches (outside the events); median of `reps`."""
+    """Every op at its BASELINE config shape: 5 warm-up launches, then `reps`
+    launches each between two HIP events on the launch stream, with a 512 MB
+    cache-flush write between launches (outside the events); median, p10, p90."""
     import torch
     s = torch.cuda.current_stream()
     flush = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
@@ -123,7 +125,7 @@ def bench_ops(ctx, reps: int, out_path: str | None) -> list:
         return (torch.randn(shape, generator=g, device="cuda") * std + mean).to(torch.bfloat16)
 
     def timed(fn):
-        for _ in range(3):
+        for _ in range(5):
             fn()
         ts = []
         for _ in range(reps):
@@ -135,16 +137,20 @@ def bench_ops(ctx, reps: int, out_path: str | None) -> list:
             e1.synchronize()
             ts.append(e0.elapsed_time(e1) * 1e3)
         ts.sort()
-        return ts[len(ts) // 2]
+        pick = lambda f: ts[min(len(ts) - 1, int(f * len(ts)))]
+        return pick(0.5), pick(0.1), pick(0.9)
 
     rows = []
 
-    def add(op, kernel, shape, nbytes, us, note=""):
+    def add(op, kernel, shape, nbytes, t, note=""):
+        us, p10, p90 = t
         gbs = nbytes / (us * 1e-6) / 1e9
         rows.append({"op": op, "kernel": kernel, "shape": shape, "bytes": int(nbytes),
-                     "us": round(us, 2), "gbs": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1),
+                     "us": round(us, 2), "us_p10": round(p10, 2), "us_p90": round(p90, 2),
+                     "gbs": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1),
                      "note": note})
-        log(f"{op:34s} {us:9.2f} us {gbs:8.0f} GB/s {100 * gbs / PEAK_GBS:5.1f}%  {note}")
+        log(f"{op:42s} {us:8.2f} us (p10 {p10:7.2f}, p90 {p90:7.2f}) {gbs:7.0f} GB/s "
+            f"{100 * gbs / PEAK_GBS:5.1f}%  {note}")
 
     T = 16384
     # copy ceiling
@@ -202,7 +208,7 @@ def bench_ops(ctx, reps: int, out_path: str | None) -> list:
     slab = torch.empty((T // 64) * 64 * 576, dtype=torch.bfloat16, device="cuda")
     qn = torch.empty((T, 1536), dtype=torch.bfloat16, device="cuda")
     mg = torch.empty((T, 3072), dtype=torch.bfloat16, device="cuda")
-    add("MLA prep (cfg 4, reference form)", "kern_k3_mla_prep_{head,gate}", f"T={T} [T,5184] bf16",
+    add("MLA prep (cfg 4, reference form)", "k3h_mla_prep_fused", f"T={T} [T,5184] bf16",
         T * 5184 * 2 + T * (1536 + 576 + 3072) * 2 + 4096,
         timed(lambda: ctx.mla_prep(mp, gq, gk, slots, slab, 0, qn, mg, T, page_stride=64 * 576, stream=s)))
     del mp, qn, mg
@@ -219,7 +225,7 @@ def bench_ops(ctx, reps: int, out_path: str | None) -> list:
     rs = torch.full((1,), 2.5, dtype=torch.bfloat16, device="cuda")
     idx = torch.empty((T, 8), dtype=torch.int32, device="cuda")
     wts = torch.empty((T, 8), dtype=torch.float32, device="cuda")
-    add("router top-8 (cfg 5a)", "kern_k3_router_topk", f"[{T},224]", T * 224 * 4 + 896 + 2 * T * 8 * 4,
+    add("router top-8 (cfg 5a)", "k3h_router_topk_rows", f"[{T},224]", T * 224 * 4 + 896 + 2 * T * 8 * 4,
         timed(lambda: ctx.router_topk(Sx, bias, rs, idx, wts, T, topk=8, stream=s)),
         "latency-bound (sequential picks)")
     E, nblk = 56, T // 256
@@ -237,12 +243,12 @@ def bench_ops(ctx, reps: int, out_path: str | None) -> list:
         ctx.moe_route_count(idx, T, 0, E, bc, topk=8, stream=s)
         ctx.moe_route_tables(bc, nblk, E, 128, bo, cb, cl, nne, tp, rmap, stream=s)
         ctx.moe_route_scatter(idx, bo, T, 0, E, rmap, e2p, topk=8, stream=s)
-    us_route = timed(route)
+    t_route = timed(route)
     torch.cuda.synchronize()
     tpad = int(tp.item())
     live = int((e2p >= 0).sum().item())
     add("EP routing tables (count+tables+scatter)", "kern_k3_moe_route_{count,tables,scatter}",
-        f"T={T} top-8 E=56", 2 * T * 8 * 4 + 3 * nblk * E * 4 + tpad * 4, us_route,
+        f"T={T} top-8 E=56", 2 * T * 8 * 4 + 3 * nblk * E * 4 + tpad * 4, t_route,
         "latency-bound (three launches, one single-workgroup scan)")
     x8 = torch.randint(0, 256, (T, H), dtype=torch.uint8, device="cuda", generator=g)
     sf8 = torch.randint(0, 256, (T, H // 32), dtype=torch.uint8, device="cuda", generator=g)
@@ -260,6 +266,77 @@ def bench_ops(ctx, reps: int, out_path: str | None) -> list:
         with open(out_path, "w") as f:
             json.dump(rows, f, indent=1)
     return rows
+
+
+# Per-op kernels, in launch order, for the counter table (kernel names as the
+# rocprofv3 CSV output prints them).
+OP_KERNELS = {
+    "stream copy (ceiling)": ["k3h_stream_copy"],
+    "residual add + RMSNorm (cfg 1)": ["kern_k3_land_add_attnres_rms"],
+    "residual+RMSNorm+MXFP8 (cfg 2)": ["k3h_residual_rms_mxfp8"],
+    "MXFP8 quant alone": ["kern_k3_moe_quant"],
+    "per-tensor fp8 pair (amax+apply)": ["kern_quant_fp8_amax_v2", "kern_quant_fp8_apply_v2"],
+    "KDA span gather (cfg 3a)": ["kern_k3_span_gather"],
+    "KDA output gate (cfg 3b)": ["kern_k3_kda_out_gate"],
+    "MLA prep (cfg 4, reference form)": ["k3h_mla_prep_fused"],
+    "MLA latent norm + RoPE + q pack": ["k3h_mla_rope_pack"],
+    "router top-8 (cfg 5a)": ["k3h_router_topk_rows"],
+    "EP routing tables (count+tables+scatter)": ["kern_k3_moe_route_count", "kern_k3_moe_route_tables",
+                                                 "kern_k3_moe_route_scatter"],
+    "MXFP8 permute (cfg 5c)": ["k3h_moe_permute_mx"],
+    "weighted finalize (cfg 5d)": ["kern_k3_moe_finalize"],
+}
+
+
+def _csv_rows(path: str):
+    import csv
+    with open(path, newline="") as f:
+        yield from csv.DictReader(f)
+
+
+def _col(row: dict, *names: str) -> str:
+    low = {k.lower(): v for k, v in row.items()}
+    for n in names:
+        if n.lower() in low:
+            return low[n.lower()]
+    raise KeyError(f"none of {names} in {sorted(row)}")
+
+
+def counter_medians(csv_path: str, counter: str) -> dict:
+    """Per kernel name: median over dispatches of `counter` (KiB per dispatch)
+    from a rocprofv3 --pmc CSV (counter_collection.csv)."""
+    per = {}
+    for r in _csv_rows(csv_path):
+        if _col(r, "Counter_Name") != counter:
+            continue
+        name = _col(r, "Kernel_Name").split("(")[0].strip()
+        per.setdefault(name, []).append(float(_col(r, "Counter_Value")))
+    return {k: sorted(v)[len(v) // 2] for k, v in per.items()}
+
+
+def traffic_table(fetch_csv: str, write_csv: str, ops_json: str) -> str:
+    """Markdown table of measured HBM bytes per op call: FETCH_SIZE and WRITE_SIZE
+    (KiB per dispatch, median), each scaled by the factor that maps the same
+    counter of k3h_stream_copy onto its known byte count, against the op's
+    algorithmic bytes (from a bench.py --ops-out JSON of the same shapes)."""
+    fetch, write = counter_medians(fetch_csv, "FETCH_SIZE"), counter_medians(write_csv, "WRITE_SIZE")
+    ops = {r["op"]: r for r in json.load(open(ops_json))}
+    copy_bytes = ops["stream copy (ceiling)"]["bytes"] // 2  # read once, written once
+    kf = copy_bytes / (fetch["k3h_stream_copy"] * 1024)
+    kw = copy_bytes / (write["k3h_stream_copy"] * 1024)
+    out = [f"Scale factors from k3h_stream_copy ({copy_bytes:,} B read and written): "
+           f"FETCH_SIZE x {kf:.5f}, WRITE_SIZE x {kw:.5f}", "",
+           "| op | kernels | read B | written B | measured B | algorithmic B | measured / algorithmic |",
+           "|---|---|---:|---:|---:|---:|---:|"]
+    for op, kernels in OP_KERNELS.items():
+        if op not in ops or any(k not in fetch or k not in write for k in kernels):
+            continue
+        rd = sum(fetch[k] for k in kernels) * 1024 * kf
+        wr = sum(write[k] for k in kernels) * 1024 * kw
+        alg = ops[op]["bytes"]
+        out.append(f"| {op} | {', '.join('`%s`' % k for k in kernels)} | {rd:,.0f} | {wr:,.0f} | "
+                   f"{rd + wr:,.0f} | {alg:,} | {(rd + wr) / alg:.3f} |")
+    return "\n".join(out)
 
 
 def load_traffic(kernel: str, workload: str):
@@ -285,7 +362,13 @@ def main() -> int:
                     help="also time every op at its config shape (table on stderr)")
     ap.add_argument("--ops-only", action="store_true", help="only the per-op table")
     ap.add_argument("--ops-out", default=None, help="write the per-op table as JSON")
+    ap.add_argument("--traffic-table", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "OPS_JSON"),
+                    help="print the per-op HBM byte table from two rocprofv3 --pmc CSVs "
+                         "(FETCH_SIZE, WRITE_SIZE runs of --ops-only) and an --ops-out JSON; no GPU")
     a = ap.parse_args()
+    if a.traffic_table:
+        print(traffic_table(*a.traffic_table))
+        return 0
     if a.gpus != 1:
         print(f"bench.py measures one GPU only (asked for {a.gpus}); the op family shards "
               "by rows / heads / experts with no exchange on the measured path.", file=sys.stderr)
@@ -297,7 +380,7 @@ def main() -> int:
     ctx = k3h.Ctx()
     rows = a.rows
     if a.ops_only:
-        bench_ops(ctx, max(5, min(a.steps, 30)), a.ops_out)
+        bench_ops(ctx, max(5, a.steps), a.ops_out)
         return 0
     copy_gbs = copy_ceiling(ctx, rows, a.steps if a.op == "copy" else 20)
     if a.op == "copy":
@@ -335,7 +418,7 @@ def main() -> int:
             "avg_launch_us": round(ms * 1e3, 2), "copy_ceiling_gbs": round(copy_gbs, 1)}
     ops = None
     if a.ops:
-        ops = bench_ops(ctx, 20, a.ops_out)
+        ops = bench_ops(ctx, 50, a.ops_out)
     cpu = None
     if not a.no_cpu:
         log("CPU baseline: C oracle on the same inputs")
