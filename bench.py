@@ -4,8 +4,9 @@
 
 A step is one launch of ``k3h_residual_rms_mxfp8`` over the whole [16384, 7168]
 chunk with inputs resident in HBM.  Timing: W untimed
-warm-up steps, then K steps between two HIP events on the launch stream, with a
-device synchronisation on both sides.  ``value`` is the effective HBM bandwidth
+warm-up steps (continued in batches of 100 until --warm-s seconds of launches
+have run, so the clocks are at steady state), then K steps between two HIP
+events on the launch stream, with a device synchronisation on both sides.  ``value`` is the effective HBM bandwidth
 (algorithmic bytes per step / mean step time).  Algorithmic bytes: x and the
 residual read once, gamma once, residual_out + e4m3 payload + E8M0 scales
 written once = 825,767,936 B.
@@ -353,6 +354,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warm-s", type=float, default=0.3,
+                    help="keep warming up (batches of 100 steps) until this many seconds have run")
     ap.add_argument("--rows", type=int, default=T)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
@@ -397,9 +400,20 @@ def main() -> int:
     def step():
         ctx.residual_rms_mxfp8(x, res, gamma, ro, q, sf, None, eps=1e-6, B=rows, stream=stream)
 
+    # W warm-up steps, continued in batches of 100 until at least --warm-s seconds
+    # of launches have run: the first ~0.1 s of a burst runs below steady clocks.
+    t_warm = time.perf_counter()
+    n_warm = 0
     for _ in range(a.warmup):
         step()
     torch.cuda.synchronize()
+    n_warm += a.warmup
+    while time.perf_counter() - t_warm < a.warm_s:
+        for _ in range(100):
+            step()
+        torch.cuda.synchronize()
+        n_warm += 100
+    log(f"warm-up: {n_warm} launches in {time.perf_counter() - t_warm:.2f} s")
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
     for _ in range(a.steps):
@@ -426,7 +440,7 @@ def main() -> int:
         log(f"CPU {cpu['value']} GB/s on {cpu['cores']} threads; {cpu['sample']}")
     line = {
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1,
-        "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 5),
+        "steps": a.steps, "warmup": a.warmup, "warmup_launches": n_warm, "ms_per_step": round(ms, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (torch randn from seed 24301; 0.1% outliers x50)",
         "config": {"workload": "fused residual add + RMSNorm + MXFP8 (BASELINE config 2)",

@@ -91,6 +91,74 @@ K3H_API int k3h_attnres_rms(k3h_ctx_t ctx, void* stream, const void* prefix, voi
 K3H_API int k3h_land_add2(k3h_ctx_t ctx, void* stream, const float* p1, const float* p2,
                           const void* prefix2, void* hidden, int two, int B);
 
+/* ---- residual push family (res_in / res_mlp of the TP4 prefill) -------------
+ * kern_k3_attnres_rms_push: K1a's row body whose normed row b lands at row
+ * rank*B + b of every rank's normed_all [nranks*B, 7168]: the local copy via
+ * normed_all, rank q != rank via dst_peer[q] (u64 device addresses, nranks <= 8;
+ * on one GPU they may all be local buffers).  grid (B), block 128, eps 1e-5.
+ *   version 1 / 3: modules k3_residual_push / k3_residual_push_v3
+ *     (k3_residual_push.cu:320, k3_residual_push_v3.cu:324; manifest op
+ *     attnres_rms_push_first_v3, k3-tp4-prefill-16k.json:406806);
+ *   k3h_attnres_rms_push_stats: module k3_residual_push_stats
+ *     (k3_residual_push_stats.cu:354): also stats [B,8,2] f32 = (sum x^2,
+ *     sum x*sw_mlp) of block candidates c < nb;
+ *   k3h_attnres_rms_push_add2: module k3_residual_push_add2
+ *     (k3_residual_push_add2.cu:362; op attnres_rms_push_add2, json:407299): the
+ *     prefix row is hidden = bf16(prefix2 + p1 [+ p2]) (bf16 inputs), also stored. */
+K3H_API int k3h_attnres_rms_push(k3h_ctx_t ctx, void* stream, int version, const void* prefix,
+                                 void* blocks, const float* sw, const void* gamma,
+                                 void* normed_all, const unsigned long long* dst_peer, int nb,
+                                 int snapshot, int B, int rank, int nranks);
+K3H_API int k3h_attnres_rms_push_stats(k3h_ctx_t ctx, void* stream, const void* prefix,
+                                       void* blocks, const float* sw, const void* gamma,
+                                       void* normed_all, const unsigned long long* dst_peer,
+                                       int nb, int snapshot, int B, int rank, int nranks,
+                                       const float* sw_mlp, float* stats);
+K3H_API int k3h_attnres_rms_push_add2(k3h_ctx_t ctx, void* stream, void* blocks, const float* sw,
+                                      const void* gamma, void* normed_all,
+                                      const unsigned long long* dst_peer, int nb, int snapshot,
+                                      int B, int rank, int nranks, const float* sw_mlp,
+                                      float* stats, const void* p1, const void* p2,
+                                      const void* prefix2, void* hidden, int two);
+/* kern_k3_land_add_attnres_rms_nb{1..8} of module k3_residual_nb_stats (LAND_BF16)
+ * (k3_residual_nb_stats.cu:366-811; ops land_add_attnres_rms_bf16_v2_nb4..8,
+ * json:406999): as k3h_land_add_attnres_rms_nb, with candidates c < nb_stats
+ * (0 <= nb_stats <= nb) scored from stats [B,8,2] written by res_in. */
+K3H_API int k3h_land_add_attnres_rms_nb_stats(k3h_ctx_t ctx, void* stream, const void* partial,
+                                              const void* prefix, const void* blocks,
+                                              const float* sw, const void* gamma, void* prefix2,
+                                              void* normed, int nb, int snapshot, int B,
+                                              const float* stats, int nb_stats);
+/* kern_k3_land_add2_bf16 (k3_land_bf16.cu:96; module k3_land_bf16): K1c with
+ * bf16 partials.  grid (B, 1), block 128. */
+K3H_API int k3h_land_add2_bf16(k3h_ctx_t ctx, void* stream, const void* p1, const void* p2,
+                               const void* prefix2, void* hidden, int two, int B);
+
+/* ---- landing kernels (shared-expert MLP, MoE latent norm) -------------------
+ * kern_k3_rms (k3_land.cu:104; l0-bf16 op rms, json:399525): o = bf16(x * r) (x)
+ * gamma, r = 1/sqrt(sum x^2 / h + 1e-5); x, o [B, h] bf16.  grid (B), block 1024. */
+K3H_API int k3h_rms(k3h_ctx_t ctx, void* stream, const void* x, const void* gamma, void* o, int h,
+                    int B);
+/* kern_k3_land (k3_land.cu:168; l0-bf16 op land_n3584, json:400710):
+ * o[b, i] = bf16(p[b*ldc + off + i]), i < n.  grid (B, ceil(n/1024)), block 1024. */
+K3H_API int k3h_land(k3h_ctx_t ctx, void* stream, const float* p, void* o, int n, int off, int ldc,
+                     int B);
+/* SiTU landing act[b, i] = bf16(4 tanh(g/4) sigmoid(g) * 25 tanh(u/25)), gate g and
+ * up u the two halves of row b of p [B, 2n] (landed to bf16 first).  bf16_in:
+ *   0  kern_k3_land_situ, p f32 (k3_land.cu:211; op land_situ_n33792,
+ *      k3-tp4-prefill-16k.json:405746; l0 op land_situ_n6144, json:400768);
+ *   1  kern_k3_land_situ_bf16, p bf16 (k3_land_bf16.cu:56; module k3_land_bf16);
+ *   2  kern_k3_situ_bf16, p bf16 (k3_situ_bf16.cu:9; l0 op land_situ_n33792,
+ *      json:400660).
+ * grid (B, ceil(n/1024)), block 1024. */
+K3H_API int k3h_land_situ(k3h_ctx_t ctx, void* stream, int bf16_in, const void* p, void* act,
+                          int n, int B);
+/* kern_k3_situ_rms_bf16 (k3_land_fused.cu:151; op land_situ_rms, json:406727): the
+ * bf16 SiTU landing of sp [B, 2n] -> act [B, n] and the rms of lat [L, h] -> ln
+ * in one launch.  grid 3 ceil(tokens/16), block 512; needs 4 ceil(tokens/16) >= B, L. */
+K3H_API int k3h_situ_rms(k3h_ctx_t ctx, void* stream, const void* sp, void* act, const void* lat,
+                         const void* gam, void* ln, int n, int B, int h, int L, int tokens);
+
 /* ---- MXFP8 -----------------------------------------------------------------
  * kern_k3_moe_quant (k3_moe_prefill_v4.cu:111; manifest op moe_quant, json:404926).
  * grid ceil(rows*cols/32/256), block 256; rows*cols % 32 == 0. */

@@ -32,6 +32,11 @@ ARCH = "gfx950"
 SOURCES = {
     "k3_residual_v2": "k3_residual_v2.hip",
     "k3_residual_nb": "k3_residual_nb.hip",
+    "k3_residual_nb_stats": "k3_residual_nb.hip",
+    "k3_residual_push": "k3_residual_push.hip",
+    "k3_residual_push_v3": "k3_residual_push.hip",
+    "k3_residual_push_stats": "k3_residual_push.hip",
+    "k3_residual_push_add2": "k3_residual_push.hip",
     "k3h_fused": "k3h_fused.hip",
     "k3_moe_prefill_v3": "k3_moe_prefill.hip",
     "k3_moe_prefill_v4": "k3_moe_prefill.hip",
@@ -43,10 +48,23 @@ SOURCES = {
     "k3_mla_prep_v2": "k3_mla_prep.hip",
     "k3_mla_prep_bf16": "k3_mla_prep.hip",
     "k3h_mla_rope": "k3h_mla_rope.hip",
+    "k3_land": "k3_land.hip",
+    "k3_land_bf16": "k3_land.hip",
+    "k3_situ_bf16": "k3_land.hip",
+    "k3_land_fused": "k3_land.hip",
 }
 
 # defines implied by a base name that shares its source with another base
 IMPLIED = {
+    "k3_land": ["-DK3_LAND_MODULE=1"],
+    "k3_land_bf16": ["-DK3_LAND_MODULE=2"],
+    "k3_situ_bf16": ["-DK3_LAND_MODULE=3"],
+    "k3_land_fused": ["-DK3_LAND_MODULE=4"],
+    "k3_residual_nb_stats": ["-DK3_NB_STATS=1", "-DLAND_BF16=1"],  # kernels.toml: defines { LAND_BF16 = 1 }
+    "k3_residual_push": ["-DK3_PUSH=1"],
+    "k3_residual_push_v3": ["-DK3_PUSH=1"],
+    "k3_residual_push_stats": ["-DK3_PUSH=2"],
+    "k3_residual_push_add2": ["-DK3_PUSH=3"],
     "k3_quant_fp8_pair_v2": ["-DK3_QUANT_V2=1"],
     "k3_mla_prep_bf16": ["-DK3_MLA_BF16=1"],
 }
@@ -58,6 +76,11 @@ MODULES = [
     "k3_residual_v2+K3_EPS=1e-6f",
     "k3_residual_v2+LAND_BF16=1+K3_EPS=1e-6f",
     "k3_residual_nb+LAND_BF16=1",
+    "k3_residual_nb_stats",
+    "k3_residual_push",
+    "k3_residual_push_v3",
+    "k3_residual_push_stats",
+    "k3_residual_push_add2",
     "k3h_fused",
     "k3_moe_prefill_v3+EP_STRIDED=1",
     "k3_moe_prefill_v4+EP_RANKS=4+EP_STRIDED=1+TILE_SHIFT=7+SCATTER_WARPS=16",
@@ -71,6 +94,10 @@ MODULES = [
     "k3_mla_prep_v2+INNER=3072+MLA_FUSED=5184",
     "k3_mla_prep_bf16+INNER=3072+MLA_FUSED=5184",
     "k3h_mla_rope",
+    "k3_land",
+    "k3_land_bf16",
+    "k3_situ_bf16",
+    "k3_land_fused",
 ]
 
 DEVICE_FLAGS = [
@@ -81,7 +108,7 @@ DEVICE_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
-HOST_SOURCES = ["k3h_module.cpp", "k3h_ops_residual.cpp", "k3h_ops_quant.cpp", "k3h_ops_moe.cpp", "k3h_ops_kda.cpp", "k3h_ops_mla.cpp"]
+HOST_SOURCES = ["k3h_module.cpp", "k3h_ops_residual.cpp", "k3h_ops_push.cpp", "k3h_ops_land.cpp", "k3h_ops_quant.cpp", "k3h_ops_moe.cpp", "k3h_ops_kda.cpp", "k3h_ops_mla.cpp"]
 
 
 def module_defines(key: str) -> tuple[str, list[str]]:

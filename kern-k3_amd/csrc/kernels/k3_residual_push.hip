@@ -1,0 +1,111 @@
+// Modules k3_residual_push, k3_residual_push_v3, k3_residual_push_stats and
+// k3_residual_push_add2: res_in, the attention residual + RMSNorm whose normed
+// row is stored into every TP rank's `normed_all` (the all-gather folded into
+// the producer).  One entry per module, `kern_k3_attnres_rms_push`, with the
+// module's parameter list:
+//
+//   push, push_v3 (K3_PUSH = 1; k3_residual_push.cu:320, k3_residual_push_v3.cu:324):
+//     (prefix, blocks, sw, gamma, normed_all, dst_peer, nb, snapshot, B, rank, nranks)
+//   push_stats (K3_PUSH = 2; k3_residual_push_stats.cu:354):
+//     (prefix, blocks, sw, gamma, normed_all, dst_peer, nb, snapshot, B, rank, nranks,
+//      sw_mlp, stats)
+//   push_add2 (K3_PUSH = 3; k3_residual_push_add2.cu:362; manifest op attnres_rms_push_add2):
+//     (blocks, sw, gamma, normed_all, dst_peer, nb, snapshot, B, rank, nranks,
+//      sw_mlp, stats, p1, p2, prefix2, hidden, two)
+//
+// grid (B, 1, 1), block (128, 1, 1) (manifest ceil_div(tokens, 4) rows per rank).
+//
+// Row b of this rank lands at row rank * B + b of every rank's normed_all: the
+// local copy through `normed_all`, the others through dst_peer[q] (q < nranks,
+// q != rank; nranks is capped at 8), each a device address of rank q's
+// normed_all (an xGMI peer mapping on a multi-GPU node).  The arithmetic is the
+// K1a row body (kern_k3_attnres_rms); push_stats also writes the candidates'
+// (sum x^2, sum x * sw_mlp) to stats[b] for res_mlp, and push_add2 first forms
+// the row as hidden = bf16(f32(prefix2) + f32(p1) [+ f32(p2)]) (bf16 inputs,
+// left to right, one rounding; kern_k3_land_add2_bf16), stores it to `hidden`
+// and uses it as the prefix candidate.  With snapshot and nb < 8 the prefix row
+// is copied to blocks[b, nb] first.  No fence: the stores are released by the
+// arrival barrier, a later launch on the same stream.
+#include "k3_residual_row.h"
+
+#ifndef K3_PUSH
+#define K3_PUSH 1
+#endif
+
+#define K3_PUSH_EPS 1e-5f
+
+#if K3_PUSH == 3
+// hidden = bf16(f32(prefix2) + f32(p1) [+ f32(p2)]) for this thread's vectors.
+K3_DEV void k3_push_land_add2(const uint16_t* __restrict__ p1, const uint16_t* __restrict__ p2,
+                              const uint16_t* __restrict__ prefix2, uint16_t* __restrict__ hidden,
+                              int two, size_t row, int t, k3_u4* pv) {
+#pragma unroll
+  for (int v = 0; v < K3_KVPT; ++v) {
+    const size_t off = row + k3_vec_off(t, v);
+    const k3_u4 a = k3_ld16_nt(p1 + off);
+    const k3_u4 c = k3_ld16_nt(prefix2 + off);
+    k3_u4 e = {0u, 0u, 0u, 0u};
+    if (two) e = k3_ld16_nt(p2 + off);
+    k3_u4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float x = k3_bf_lo(c[j]) + k3_bf_lo(a[j]);
+      float y = k3_bf_hi(c[j]) + k3_bf_hi(a[j]);
+      if (two) {
+        x += k3_bf_lo(e[j]);
+        y += k3_bf_hi(e[j]);
+      }
+      o[j] = k3_pack_bf2(x, y);
+    }
+    pv[v] = o;
+    k3_st16(hidden + off, o);
+  }
+}
+#endif
+
+extern "C" __global__ void __launch_bounds__(K3_RES_THREADS) kern_k3_attnres_rms_push(
+#if K3_PUSH != 3
+    const uint16_t* __restrict__ prefix,
+#endif
+    uint16_t* __restrict__ blocks, const float* __restrict__ sw,
+    const uint16_t* __restrict__ gamma, uint16_t* __restrict__ normed_all,
+    const unsigned long long* __restrict__ dst_peer, int nb, int snapshot, int B, int rank,
+    int nranks
+#if K3_PUSH >= 2
+    , const float* __restrict__ sw_mlp, float* __restrict__ stats
+#endif
+#if K3_PUSH == 3
+    , const uint16_t* __restrict__ p1, const uint16_t* __restrict__ p2,
+    const uint16_t* __restrict__ prefix2, uint16_t* __restrict__ hidden, int two
+#endif
+) {
+  const int b = blockIdx.x;
+  if (b >= B) return;
+  if (nb < 0 || nb > K3_NB_MAX) return;
+  const int t = threadIdx.x;
+  const int nr = nranks < K3_MAX_RANKS ? nranks : K3_MAX_RANKS;
+  const long long dst_off = ((long long)rank * B + b) * K3_H;
+  const size_t row = (size_t)b * K3_H;
+
+  k3_u4 pv[K3_KVPT];
+#if K3_PUSH == 3
+  k3_push_land_add2(p1, p2, prefix2, hidden, two, row, t, pv);
+#else
+#pragma unroll
+  for (int v = 0; v < K3_KVPT; ++v) pv[v] = k3_ld16_nt(prefix + row + k3_vec_off(t, v));
+#endif
+  if (snapshot && nb < K3_NB_MAX) {
+#pragma unroll
+    for (int v = 0; v < K3_KVPT; ++v)
+      k3_st16(blocks + ((size_t)b * K3_NB_MAX + nb) * K3_H + k3_vec_off(t, v), pv[v]);
+  }
+  const K3NormedDst dst = {normed_all + dst_off, dst_peer, dst_off, rank, nr};
+#if K3_PUSH >= 2
+  k3_attnres_rms_row_to<-1, K3_MIX_STATS_OUT>(blocks + (size_t)b * K3_NB_MAX * K3_H, pv, sw, gamma,
+                                              dst, nb, K3_PUSH_EPS, t, sw_mlp,
+                                              stats + (size_t)b * K3_NB_MAX * 2);
+#else
+  k3_attnres_rms_row_to<-1>(blocks + (size_t)b * K3_NB_MAX * K3_H, pv, sw, gamma, dst, nb,
+                            K3_PUSH_EPS, t);
+#endif
+}

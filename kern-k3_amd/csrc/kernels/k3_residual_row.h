@@ -74,24 +74,55 @@ K3_DEV float k3_row_rscale(float tot, float eps) {
 
 // AttnRes mixing: replaces pv (the prefix candidate) by the mixed row.
 // NBC >= 0 fixes nb at compile time; NBC < 0 takes the run-time nb.
-template <int NBC>
+//
+// MODE selects the candidate-statistics hand-off between the attention
+// residual (res_in) and the MLP residual (res_mlp) of one layer
+// (k3_residual_push_stats.cu:176-263, k3_residual_nb_stats.cu:176-258):
+//   K3_MIX_STATS_OUT: for every block candidate c < nb also accumulate
+//     dm_c = sum x * sw_mlp (same per-thread order and butterfly as dp_c) and
+//     write stats_out[c] = (sq_c, dm_c), the half-wave-0 totals;
+//   K3_MIX_STATS_IN: candidates c < ns = min(nb_stats, nb) take (sq_c, dp_c)
+//     from stats_in[c] instead of reading their rows in pass 1 (pass 2 still
+//     reads every candidate).  Given statistics produced by STATS_OUT with
+//     sw_mlp equal to this call's sw, the result is bit-identical to MODE 0.
+// stats rows are [K3_NB_MAX][2] floats.
+#define K3_MIX_STATS_OUT 1
+#define K3_MIX_STATS_IN 2
+
+template <int NBC, int MODE = 0>
 K3_DEV void k3_attnres_mix(const uint16_t* __restrict__ blk_row, k3_u4* pv,
-                           const float* __restrict__ sw, int nb_rt, float eps, int t) {
+                           const float* __restrict__ sw, int nb_rt, float eps, int t,
+                           const float* __restrict__ sw_mlp = nullptr,
+                           float* __restrict__ stats_out = nullptr,
+                           const float* __restrict__ stats_in = nullptr, int nb_stats = 0) {
+  constexpr bool SOUT = (MODE & K3_MIX_STATS_OUT) != 0;
+  constexpr bool SIN = (MODE & K3_MIX_STATS_IN) != 0;
   const int nb = NBC >= 0 ? NBC : nb_rt;
   if (nb <= 0) return;  // mixed = prefix: bf16(1.0f * f32(prefix)) == prefix
+  const int ns = SIN ? (nb_stats < 0 ? 0 : nb_stats < nb ? nb_stats : nb) : 0;
   __shared__ float s_red[(K3_NB_MAX + 1) * 2 * K3_NHW];
+  __shared__ float s_redm[SOUT ? K3_NB_MAX * K3_NHW : 1];
   const int lane32 = t & 31, hw = t >> 5;
 
   // pass 1: sum x^2 and sum x * sw per candidate (prefix kept at index K3_NB_MAX)
-  float sq[K3_NB_MAX + 1], dp[K3_NB_MAX + 1];
+  float sq[K3_NB_MAX + 1], dp[K3_NB_MAX + 1], dm[K3_NB_MAX];
 #pragma unroll
   for (int c = 0; c <= K3_NB_MAX; ++c) { sq[c] = 0.0f; dp[c] = 0.0f; }
+#pragma unroll
+  for (int c = 0; c < K3_NB_MAX; ++c) dm[c] = 0.0f;
 #pragma unroll
   for (int v = 0; v < K3_KVPT; ++v) {
     const int u = k3_vec_off(t, v);
     const float4 a = *(const float4*)(sw + u);
     const float4 b = *(const float4*)(sw + u + 4);
     const float swv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    float swm[8];
+    if (SOUT) {
+      const float4 ma = *(const float4*)(sw_mlp + u);
+      const float4 mb = *(const float4*)(sw_mlp + u + 4);
+      swm[0] = ma.x; swm[1] = ma.y; swm[2] = ma.z; swm[3] = ma.w;
+      swm[4] = mb.x; swm[5] = mb.y; swm[6] = mb.z; swm[7] = mb.w;
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float lo = k3_bf_lo(pv[v][j]), hi = k3_bf_hi(pv[v][j]);
@@ -103,6 +134,7 @@ K3_DEV void k3_attnres_mix(const uint16_t* __restrict__ blk_row, k3_u4* pv,
 #pragma unroll
     for (int c = 0; c < K3_NB_MAX; ++c) {
       if (c >= nb) break;
+      if (SIN && c < ns) continue;
       const k3_u4 x = k3_ld16(blk_row + (size_t)c * K3_H + u);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -111,15 +143,24 @@ K3_DEV void k3_attnres_mix(const uint16_t* __restrict__ blk_row, k3_u4* pv,
         sq[c] = __builtin_fmaf(hi, hi, sq[c]);
         dp[c] = __builtin_fmaf(lo, swv[2 * j], dp[c]);
         dp[c] = __builtin_fmaf(hi, swv[2 * j + 1], dp[c]);
+        if (SOUT) {
+          dm[c] = __builtin_fmaf(lo, swm[2 * j], dm[c]);
+          dm[c] = __builtin_fmaf(hi, swm[2 * j + 1], dm[c]);
+        }
       }
     }
   }
 #pragma unroll
   for (int c = 0; c < K3_NB_MAX; ++c) {
     if (c >= nb) break;
+    if (SIN && c < ns) continue;
     const float s = k3_sum32(sq[c]);
     const float d = k3_sum32(dp[c]);
     if (lane32 == 0) { s_red[(2 * c) * K3_NHW + hw] = s; s_red[(2 * c + 1) * K3_NHW + hw] = d; }
+    if (SOUT) {
+      const float m = k3_sum32(dm[c]);
+      if (lane32 == 0) s_redm[c * K3_NHW + hw] = m;
+    }
   }
   {
     const float s = k3_sum32(sq[K3_NB_MAX]);
@@ -133,10 +174,22 @@ K3_DEV void k3_attnres_mix(const uint16_t* __restrict__ blk_row, k3_u4* pv,
   float sc = -3.0e38f;
   if (lane32 < ncand) {
     float sqv = 0.0f, dpv = 0.0f;
+    if (SIN && lane32 < ns) {
+      sqv = stats_in[2 * lane32];
+      dpv = stats_in[2 * lane32 + 1];
+    } else {
 #pragma unroll
-    for (int w = 0; w < K3_NHW; ++w) {
-      sqv += s_red[(2 * lane32) * K3_NHW + w];
-      dpv += s_red[(2 * lane32 + 1) * K3_NHW + w];
+      for (int w = 0; w < K3_NHW; ++w) {
+        sqv += s_red[(2 * lane32) * K3_NHW + w];
+        dpv += s_red[(2 * lane32 + 1) * K3_NHW + w];
+      }
+    }
+    if (SOUT && hw == 0 && lane32 < nb) {
+      float dmv = 0.0f;
+#pragma unroll
+      for (int w = 0; w < K3_NHW; ++w) dmv += s_redm[lane32 * K3_NHW + w];
+      stats_out[2 * lane32] = sqv;
+      stats_out[2 * lane32 + 1] = dmv;
     }
     sc = dpv * k3_row_rscale(sqv, eps);
   }
@@ -194,19 +247,52 @@ K3_DEV void k3_rms_apply(const k3_u4* pv, const uint16_t* __restrict__ gamma, fl
   }
 }
 
-// The whole row body: mixing (if any), RMS, normed store.
-template <int NBC>
-K3_DEV void k3_attnres_rms_row(const uint16_t* __restrict__ blk_row, k3_u4* pv,
-                               const float* __restrict__ sw, const uint16_t* __restrict__ gamma,
-                               uint16_t* __restrict__ normed_row, int nb, float eps, int t) {
+// Where a row body stores its normed row: `row`, and, for the push entries, the
+// same row offset `off` of every other rank's buffer peer[q], q < nr, q != rank
+// (k3_residual_push_v3.cu:306-312).  peer == nullptr: the local row only.
+#define K3_MAX_RANKS 8
+struct K3NormedDst {
+  uint16_t* row;
+  const unsigned long long* peer;
+  long long off;
+  int rank, nr;
+};
+
+// The whole row body: mixing (if any), RMS, normed store(s).  MODE, sw_mlp and
+// the stats arguments are those of k3_attnres_mix.
+template <int NBC, int MODE = 0>
+K3_DEV void k3_attnres_rms_row_to(const uint16_t* __restrict__ blk_row, k3_u4* pv,
+                                  const float* __restrict__ sw, const uint16_t* __restrict__ gamma,
+                                  const K3NormedDst& dst, int nb, float eps, int t,
+                                  const float* __restrict__ sw_mlp = nullptr,
+                                  float* __restrict__ stats_out = nullptr,
+                                  const float* __restrict__ stats_in = nullptr, int nb_stats = 0) {
   __shared__ float s_red2[K3_NHW];
-  k3_attnres_mix<NBC>(blk_row, pv, sw, nb, eps, t);
+  k3_attnres_mix<NBC, MODE>(blk_row, pv, sw, nb, eps, t, sw_mlp, stats_out, stats_in, nb_stats);
   const float tot = k3_block_sum128(k3_row_sumsq(pv), s_red2, t);
   const float r = k3_row_rscale(tot, eps);
   k3_u4 nv[K3_KVPT];
   k3_rms_apply(pv, gamma, r, nv, t);
 #pragma unroll
-  for (int v = 0; v < K3_KVPT; ++v) k3_st16_nt(normed_row + k3_vec_off(t, v), nv[v]);
+  for (int v = 0; v < K3_KVPT; ++v) k3_st16_nt(dst.row + k3_vec_off(t, v), nv[v]);
+  if (dst.peer) {
+#pragma unroll
+    for (int q = 0; q < K3_MAX_RANKS; ++q) {
+      if (q >= dst.nr) break;
+      if (q == dst.rank) continue;
+      uint16_t* prow = (uint16_t*)(uintptr_t)dst.peer[q] + dst.off;
+#pragma unroll
+      for (int v = 0; v < K3_KVPT; ++v) k3_st16_nt(prow + k3_vec_off(t, v), nv[v]);
+    }
+  }
+}
+
+template <int NBC>
+K3_DEV void k3_attnres_rms_row(const uint16_t* __restrict__ blk_row, k3_u4* pv,
+                               const float* __restrict__ sw, const uint16_t* __restrict__ gamma,
+                               uint16_t* __restrict__ normed_row, int nb, float eps, int t) {
+  const K3NormedDst dst = {normed_row, nullptr, 0, 0, 1};
+  k3_attnres_rms_row_to<NBC>(blk_row, pv, sw, gamma, dst, nb, eps, t);
 }
 
 // K1b landing: prefix2 = snapshot ? bf16(pf) : bf16(f32(prefix) + f32(bf16(pf))).
@@ -241,15 +327,19 @@ K3_DEV k3_u4 k3_add_land(k3_u4 prefix, k3_u4 landed) {
   return o;
 }
 
-// K1b entry body shared by the run-time-nb entry and the per-nb entries.
-template <int NBC>
+// K1b entry body shared by the run-time-nb entry and the per-nb entries.  With
+// MODE = K3_MIX_STATS_IN the first nb_stats candidates' statistics come from
+// stats[b] ([B, K3_NB_MAX, 2], written by the push-stats entry of res_in).
+template <int NBC, int MODE = 0>
 K3_DEV void k3_land_add_attnres_rms_body(const k3_land_t* __restrict__ partial,
                                          const uint16_t* __restrict__ prefix,
                                          const uint16_t* __restrict__ blocks,
                                          const float* __restrict__ sw,
                                          const uint16_t* __restrict__ gamma,
                                          uint16_t* __restrict__ prefix2,
-                                         uint16_t* __restrict__ normed, int nb, int snapshot, int B) {
+                                         uint16_t* __restrict__ normed, int nb, int snapshot, int B,
+                                         const float* __restrict__ stats = nullptr,
+                                         int nb_stats = 0) {
   const int b = blockIdx.x;
   if (b >= B) return;
   const int t = threadIdx.x;
@@ -261,6 +351,10 @@ K3_DEV void k3_land_add_attnres_rms_body(const k3_land_t* __restrict__ partial,
     pv[v] = snapshot ? l : k3_add_land(k3_ld16_nt(prefix + off), l);
     k3_st16_nt(prefix2 + off, pv[v]);
   }
-  k3_attnres_rms_row<NBC>(blocks + (size_t)b * K3_NB_MAX * K3_H, pv, sw, gamma,
-                          normed + (size_t)b * K3_H, nb, K3_EPS, t);
+  const K3NormedDst dst = {normed + (size_t)b * K3_H, nullptr, 0, 0, 1};
+  const bool have_stats = MODE != 0 && stats != nullptr;  // no statistics: nb_stats acts as 0
+  k3_attnres_rms_row_to<NBC, MODE>(blocks + (size_t)b * K3_NB_MAX * K3_H, pv, sw, gamma, dst, nb,
+                                   K3_EPS, t, nullptr, nullptr,
+                                   have_stats ? stats + (size_t)b * K3_NB_MAX * 2 : nullptr,
+                                   have_stats ? nb_stats : 0);
 }

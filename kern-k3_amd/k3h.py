@@ -82,6 +82,16 @@ _SIGS: dict[str, list] = {
     "k3h_kda_out_gate": [_P, _P, _P, _P, _P, _P, _P, _I],
     "k3h_mla_prep": [_P, _P, _I, _P, _P, _P, _P, _P, ctypes.c_int64, ctypes.c_int64, _P, _P, _I],
     "k3h_mla_rope_pack": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _F, _I, _I],
+    "k3h_attnres_rms_push": [_P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I],
+    "k3h_attnres_rms_push_stats": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P],
+    "k3h_attnres_rms_push_add2": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P,
+                                  _P, _P, _I],
+    "k3h_land_add_attnres_rms_nb_stats": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _I],
+    "k3h_land_add2_bf16": [_P, _P, _P, _P, _P, _P, _I, _I],
+    "k3h_rms": [_P, _P, _P, _P, _P, _I, _I],
+    "k3h_land": [_P, _P, _P, _P, _I, _I, _I, _I],
+    "k3h_land_situ": [_P, _P, _I, _P, _P, _I, _I],
+    "k3h_situ_rms": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I],
 }
 
 
@@ -231,6 +241,135 @@ class Ctx:
                                     _ptr(hidden), two, B), "land_add2")
 
     # ------------------------------------------------------------ MXFP8
+    # ------------------------------------------------------------ push family
+    def _push_checks(self, blocks, sw, gamma, normed_all, dst_peer, nb, snapshot, B, rank, nranks):
+        if nb > 0 or (snapshot and nb < 8):
+            _dev(blocks, "blocks", BF16, B * 8 * H)
+        if nb > 0:
+            _dev(sw, "sw", F32, H)
+        _dev(gamma, "gamma", BF16, H)
+        _dev(normed_all, "normed_all", BF16, (rank + 1) * B * H)
+        if nranks > 1:
+            _dev(dst_peer, "dst_peer", I64, nranks, align=8)
+
+    def attnres_rms_push(self, prefix, blocks, sw, gamma, normed_all, dst_peer, nb: int,
+                         snapshot: int, B: int, rank: int, nranks: int, version: int = 3,
+                         stream=None) -> None:
+        """kern_k3_attnres_rms_push of k3_residual_push (version 1) / _v3 (version 3)
+        (k3_residual_push_v3.cu:324; op attnres_rms_push_first_v3).  dst_peer: int64
+        tensor of every rank's normed_all device address."""
+        _dev(prefix, "prefix", BF16, B * H)
+        self._push_checks(blocks, sw, gamma, normed_all, dst_peer, nb, snapshot, B, rank, nranks)
+        _check(self.L.k3h_attnres_rms_push(
+            self.h, _stream(stream), version, _ptr(prefix), _ptr(blocks), _ptr(sw), _ptr(gamma),
+            _ptr(normed_all), _ptr(dst_peer), nb, snapshot, B, rank, nranks), "attnres_rms_push")
+
+    def attnres_rms_push_stats(self, prefix, blocks, sw, gamma, normed_all, dst_peer, nb: int,
+                               snapshot: int, B: int, rank: int, nranks: int, sw_mlp, stats,
+                               stream=None) -> None:
+        """kern_k3_attnres_rms_push of k3_residual_push_stats (k3_residual_push_stats.cu:354)."""
+        _dev(prefix, "prefix", BF16, B * H)
+        self._push_checks(blocks, sw, gamma, normed_all, dst_peer, nb, snapshot, B, rank, nranks)
+        if nb > 0:
+            _dev(sw_mlp, "sw_mlp", F32, H)
+            _dev(stats, "stats", F32, B * 16, align=8)
+        _check(self.L.k3h_attnres_rms_push_stats(
+            self.h, _stream(stream), _ptr(prefix), _ptr(blocks), _ptr(sw), _ptr(gamma),
+            _ptr(normed_all), _ptr(dst_peer), nb, snapshot, B, rank, nranks, _ptr(sw_mlp),
+            _ptr(stats)), "attnres_rms_push_stats")
+
+    def attnres_rms_push_add2(self, blocks, sw, gamma, normed_all, dst_peer, nb: int,
+                              snapshot: int, B: int, rank: int, nranks: int, sw_mlp, stats, p1,
+                              p2, prefix2, hidden, two: int, stream=None) -> None:
+        """kern_k3_attnres_rms_push of k3_residual_push_add2 (k3_residual_push_add2.cu:362;
+        op attnres_rms_push_add2)."""
+        self._push_checks(blocks, sw, gamma, normed_all, dst_peer, nb, snapshot, B, rank, nranks)
+        if nb > 0:
+            _dev(sw_mlp, "sw_mlp", F32, H)
+            _dev(stats, "stats", F32, B * 16, align=8)
+        _dev(p1, "p1", BF16, B * H)
+        if two:
+            _dev(p2, "p2", BF16, B * H)
+        _dev(prefix2, "prefix2", BF16, B * H)
+        _dev(hidden, "hidden", BF16, B * H)
+        _check(self.L.k3h_attnres_rms_push_add2(
+            self.h, _stream(stream), _ptr(blocks), _ptr(sw), _ptr(gamma), _ptr(normed_all),
+            _ptr(dst_peer), nb, snapshot, B, rank, nranks, _ptr(sw_mlp), _ptr(stats), _ptr(p1),
+            _ptr(p2), _ptr(prefix2), _ptr(hidden), two), "attnres_rms_push_add2")
+
+    def land_add_attnres_rms_nb_stats(self, partial, prefix, blocks, sw, gamma, prefix2, normed,
+                                      nb: int, snapshot: int, B: int, stats, nb_stats: int,
+                                      stream=None) -> None:
+        """kern_k3_land_add_attnres_rms_nb{nb} of k3_residual_nb_stats (LAND_BF16)
+        (k3_residual_nb_stats.cu:366-811; ops land_add_attnres_rms_bf16_v2_nb4..8)."""
+        n = B * H
+        _dev(partial, "partial", BF16, n)
+        if not snapshot:
+            _dev(prefix, "prefix", BF16, n)
+        _dev(blocks, "blocks", BF16, B * 8 * H)
+        _dev(sw, "sw", F32, H)
+        _dev(gamma, "gamma", BF16, H)
+        _dev(prefix2, "prefix2", BF16, n)
+        _dev(normed, "normed", BF16, n)
+        if nb_stats > 0:
+            _dev(stats, "stats", F32, B * 16, align=8)
+        _check(self.L.k3h_land_add_attnres_rms_nb_stats(
+            self.h, _stream(stream), _ptr(partial), _ptr(prefix), _ptr(blocks), _ptr(sw),
+            _ptr(gamma), _ptr(prefix2), _ptr(normed), nb, snapshot, B, _ptr(stats), nb_stats),
+            "land_add_attnres_rms_nb_stats")
+
+    def land_add2_bf16(self, p1, p2, prefix2, hidden, two: int, B: int, stream=None) -> None:
+        """kern_k3_land_add2_bf16 (k3_land_bf16.cu:96)."""
+        _dev(p1, "p1", BF16, B * H)
+        if two:
+            _dev(p2, "p2", BF16, B * H)
+        _dev(prefix2, "prefix2", BF16, B * H)
+        _dev(hidden, "hidden", BF16, B * H)
+        _check(self.L.k3h_land_add2_bf16(self.h, _stream(stream), _ptr(p1), _ptr(p2),
+                                         _ptr(prefix2), _ptr(hidden), two, B), "land_add2_bf16")
+
+    # ------------------------------------------------------------ landing kernels
+    def rms(self, x, gamma, o, h: int, B: int, stream=None) -> None:
+        """kern_k3_rms (k3_land.cu:104; l0 op rms)."""
+        al = 16 if h % 8 == 0 else 2
+        _dev(x, "x", BF16, B * h, align=al)
+        _dev(gamma, "gamma", BF16, h, align=al)
+        _dev(o, "o", BF16, B * h, align=al)
+        _check(self.L.k3h_rms(self.h, _stream(stream), _ptr(x), _ptr(gamma), _ptr(o), h, B), "rms")
+
+    def land(self, p, o, n: int, off: int, ldc: int, B: int, stream=None) -> None:
+        """kern_k3_land (k3_land.cu:168; l0 op land_n3584)."""
+        vec = (n | off | ldc) % 4 == 0
+        _dev(p, "p", F32, B * ldc, align=16 if vec else 4)
+        _dev(o, "o", BF16, B * n, align=8 if vec else 2)
+        _check(self.L.k3h_land(self.h, _stream(stream), _ptr(p), _ptr(o), n, off, ldc, B), "land")
+
+    def land_situ(self, p, act, n: int, B: int, variant: str | None = None, stream=None) -> None:
+        """SiTU landing: p f32 -> kern_k3_land_situ (op land_situ_n33792); p bf16 ->
+        kern_k3_land_situ_bf16 (variant "land_bf16", default) or kern_k3_situ_bf16
+        (variant "situ_bf16", l0 op land_situ_n33792)."""
+        vec = n % 8 == 0
+        if p.dtype == torch.float32:
+            mode = 0
+        else:
+            mode = 2 if variant == "situ_bf16" else 1
+        _dev(p, "p", F32 if mode == 0 else BF16, B * 2 * n, align=16 if vec else 2)
+        _dev(act, "act", BF16, B * n, align=16 if vec else 2)
+        _check(self.L.k3h_land_situ(self.h, _stream(stream), mode, _ptr(p), _ptr(act), n, B),
+               "land_situ")
+
+    def situ_rms(self, sp, act, lat, gam, ln, n: int, B: int, h: int, L: int, tokens: int,
+                 stream=None) -> None:
+        """kern_k3_situ_rms_bf16 (k3_land_fused.cu:151; op land_situ_rms)."""
+        a_s, a_l = (16 if n % 8 == 0 else 2), (16 if h % 8 == 0 else 2)
+        _dev(sp, "sp", BF16, B * 2 * n, align=a_s)
+        _dev(act, "act", BF16, B * n, align=a_s)
+        _dev(lat, "lat", BF16, L * h, align=a_l)
+        _dev(gam, "gam", BF16, h, align=a_l)
+        _dev(ln, "ln", BF16, L * h, align=a_l)
+        _check(self.L.k3h_situ_rms(self.h, _stream(stream), _ptr(sp), _ptr(act), _ptr(lat),
+                                   _ptr(gam), _ptr(ln), n, B, h, L, tokens), "situ_rms")
+
     def moe_quant(self, x, q, sf, rows: int, cols: int, stream=None) -> None:
         """kern_k3_moe_quant (k3_moe_prefill_v4.cu:111): manifest op moe_quant."""
         n = rows * cols
@@ -496,7 +635,12 @@ class ManifestOp:
                 vals = []
                 for a in ln["args"]:
                     (k, v), = a.items()
-                    vals.append(args[v] if k == "param" else v)
+                    if k == "param":
+                        vals.append(args[v])
+                    elif k == "rank":  # this process's rank in group v ("tp" / "ep")
+                        vals.append(int(env[f"rank_{v}"]))
+                    else:
+                        vals.append(v)
             else:
                 vals = list(args)
             buf = pack_args(kinds, vals)

@@ -143,13 +143,21 @@ static inline float rscale(float tot, float eps) {
 /* attnres_rms_row (k3_residual_v2.cu:107-257).  pv holds the prefix
  * candidate (bf16 values as f32) and is replaced by the mixed row; thread t
  * of 128 owns elements 8(t + 128 v) .. +8, v < 7. */
-static void attnres_rms_row(const uint16_t* blk_row, float* pv, const float* sw,
-                            const uint16_t* gamma, uint16_t* normed_row, int nb, float eps) {
+/* sw_mlp / stats_out: res_in's hand-off (k3_residual_push_stats.cu:176-263):
+ * stats_out[c] = (sum x^2, sum x * sw_mlp) of block candidate c < nb, summed
+ * in the same order as sq / dp.  stats_in / nb_stats: res_mlp's side
+ * (k3_residual_nb_stats.cu:176-258): candidates c < min(nb_stats, nb) take
+ * (sq, dp) from stats_in[c].  Both are [NB_MAX][2]. */
+static void attnres_rms_row_ex(const uint16_t* blk_row, float* pv, const float* sw,
+                               const uint16_t* gamma, uint16_t* normed_row, int nb, float eps,
+                               const float* sw_mlp, float* stats_out, const float* stats_in,
+                               int nb_stats) {
+  const int ns = stats_in ? (nb_stats < 0 ? 0 : nb_stats < nb ? nb_stats : nb) : 0;
   if (nb > 0) {
     /* pass 1 (k3_residual_v2.cu:124-162): per-thread serial sums */
-    float sq[NB_MAX + 1][THREADS], dp[NB_MAX + 1][THREADS];
+    float sq[NB_MAX + 1][THREADS], dp[NB_MAX + 1][THREADS], dm[NB_MAX][THREADS];
     for (int t = 0; t < THREADS; ++t) {
-      float s[NB_MAX + 1] = {0}, d[NB_MAX + 1] = {0};
+      float s[NB_MAX + 1] = {0}, d[NB_MAX + 1] = {0}, m[NB_MAX] = {0};
       for (int v = 0; v < KVPT; ++v) {
         const int u = (t + v * THREADS) * 8;
         for (int j = 0; j < 8; ++j) {
@@ -157,14 +165,16 @@ static void attnres_rms_row(const uint16_t* blk_row, float* pv, const float* sw,
           s[NB_MAX] = fmaf(f, f, s[NB_MAX]);
           d[NB_MAX] = fmaf(f, sw[u + j], d[NB_MAX]);
         }
-        for (int c = 0; c < nb; ++c)
+        for (int c = ns; c < nb; ++c)
           for (int j = 0; j < 8; ++j) {
             const float f = k3o_bf2f(blk_row[(size_t)c * H + u + j]);
             s[c] = fmaf(f, f, s[c]);
             d[c] = fmaf(f, sw[u + j], d[c]);
+            if (sw_mlp) m[c] = fmaf(f, sw_mlp[u + j], m[c]);
           }
       }
       for (int c = 0; c <= NB_MAX; ++c) { sq[c][t] = s[c]; dp[c][t] = d[c]; }
+      for (int c = 0; c < NB_MAX; ++c) dm[c][t] = m[c];
     }
     /* candidate order: blocks 0..nb-1, then the prefix (k3_residual_v2.cu:154-161) */
     float sc[32], ex[32], p[NB_MAX + 1];
@@ -173,9 +183,20 @@ static void attnres_rms_row(const uint16_t* blk_row, float* pv, const float* sw,
     for (int c = 0; c < ncand; ++c) {
       const int src = c < nb ? c : NB_MAX;
       float sqv = 0.0f, dpv = 0.0f;
-      for (int w = 0; w < 4; ++w) {
-        sqv += bfly_sum(&sq[src][32 * w], 32);
-        dpv += bfly_sum(&dp[src][32 * w], 32);
+      if (c < ns) {
+        sqv = stats_in[2 * c];
+        dpv = stats_in[2 * c + 1];
+      } else {
+        for (int w = 0; w < 4; ++w) {
+          sqv += bfly_sum(&sq[src][32 * w], 32);
+          dpv += bfly_sum(&dp[src][32 * w], 32);
+        }
+      }
+      if (stats_out && c < nb) {
+        float dmv = 0.0f;
+        for (int w = 0; w < 4; ++w) dmv += bfly_sum(&dm[c][32 * w], 32);
+        stats_out[2 * c] = sqv;
+        stats_out[2 * c + 1] = dmv;
       }
       sc[c] = dpv * rscale(sqv, eps);
       mx = fmaxf(mx, sc[c]);
@@ -213,11 +234,18 @@ static void attnres_rms_row(const uint16_t* blk_row, float* pv, const float* sw,
   }
 }
 
-/* K1b kern_k3_land_add_attnres_rms (k3_residual_v2.cu:295-345). */
-void k3o_land_add_attnres_rms(const uint16_t* partial_bf16, const float* partial_f32,
-                              const uint16_t* prefix, const uint16_t* blocks,
-                              const float* sw, const uint16_t* gamma, uint16_t* prefix2,
-                              uint16_t* normed, int nb, int snapshot, int B, float eps) {
+static void attnres_rms_row(const uint16_t* blk_row, float* pv, const float* sw,
+                            const uint16_t* gamma, uint16_t* normed_row, int nb, float eps) {
+  attnres_rms_row_ex(blk_row, pv, sw, gamma, normed_row, nb, eps, NULL, NULL, NULL, 0);
+}
+
+/* K1b kern_k3_land_add_attnres_rms (k3_residual_v2.cu:295-345); with stats,
+ * the res_mlp entries of k3_residual_nb_stats.cu:366-811 (stats [B, 8, 2]). */
+void k3o_land_add_attnres_rms_stats(const uint16_t* partial_bf16, const float* partial_f32,
+                                    const uint16_t* prefix, const uint16_t* blocks,
+                                    const float* sw, const uint16_t* gamma, uint16_t* prefix2,
+                                    uint16_t* normed, int nb, int snapshot, int B, float eps,
+                                    const float* stats, int nb_stats) {
   if (nb < 0 || nb > NB_MAX) return;
 #pragma omp parallel for schedule(static)
   for (int b = 0; b < B; ++b) {
@@ -229,16 +257,28 @@ void k3o_land_add_attnres_rms(const uint16_t* partial_bf16, const float* partial
       prefix2[o] = k3o_f2bf(v);
       pv[i] = v;
     }
-    attnres_rms_row(blocks + (size_t)b * NB_MAX * H, pv, sw, gamma, normed + (size_t)b * H, nb,
-                    eps);
+    attnres_rms_row_ex(blocks + (size_t)b * NB_MAX * H, pv, sw, gamma, normed + (size_t)b * H,
+                       nb, eps, NULL, NULL, stats ? stats + (size_t)b * NB_MAX * 2 : NULL,
+                       nb_stats);
     free(pv);
   }
 }
 
-/* K1a kern_k3_attnres_rms (k3_residual_v2.cu:260-284). */
-void k3o_attnres_rms(const uint16_t* prefix, uint16_t* blocks, const float* sw,
-                     const uint16_t* gamma, uint16_t* normed, int nb, int snapshot, int B,
-                     float eps) {
+void k3o_land_add_attnres_rms(const uint16_t* partial_bf16, const float* partial_f32,
+                              const uint16_t* prefix, const uint16_t* blocks,
+                              const float* sw, const uint16_t* gamma, uint16_t* prefix2,
+                              uint16_t* normed, int nb, int snapshot, int B, float eps) {
+  k3o_land_add_attnres_rms_stats(partial_bf16, partial_f32, prefix, blocks, sw, gamma, prefix2,
+                                 normed, nb, snapshot, B, eps, NULL, 0);
+}
+
+/* K1a kern_k3_attnres_rms (k3_residual_v2.cu:260-284); with sw_mlp / stats,
+ * res_in's statistics hand-off (k3_residual_push_stats.cu:354-385).  The push
+ * entries (k3_residual_push_v3.cu:324-351) store this normed row into every
+ * rank's normed_all; the checker computes the row once. */
+void k3o_attnres_rms_stats(const uint16_t* prefix, uint16_t* blocks, const float* sw,
+                           const uint16_t* gamma, uint16_t* normed, int nb, int snapshot, int B,
+                           float eps, const float* sw_mlp, float* stats) {
   if (nb < 0 || nb > NB_MAX) return;
 #pragma omp parallel for schedule(static)
   for (int b = 0; b < B; ++b) {
@@ -246,10 +286,31 @@ void k3o_attnres_rms(const uint16_t* prefix, uint16_t* blocks, const float* sw,
     for (int i = 0; i < H; ++i) pv[i] = k3o_bf2f(prefix[(size_t)b * H + i]);
     if (snapshot && nb < NB_MAX)
       memcpy(blocks + ((size_t)b * NB_MAX + nb) * H, prefix + (size_t)b * H, 2 * H);
-    attnres_rms_row(blocks + (size_t)b * NB_MAX * H, pv, sw, gamma, normed + (size_t)b * H, nb,
-                    eps);
+    attnres_rms_row_ex(blocks + (size_t)b * NB_MAX * H, pv, sw, gamma, normed + (size_t)b * H, nb,
+                       eps, stats ? sw_mlp : NULL, stats ? stats + (size_t)b * NB_MAX * 2 : NULL,
+                       NULL, 0);
     free(pv);
   }
+}
+
+void k3o_attnres_rms(const uint16_t* prefix, uint16_t* blocks, const float* sw,
+                     const uint16_t* gamma, uint16_t* normed, int nb, int snapshot, int B,
+                     float eps) {
+  k3o_attnres_rms_stats(prefix, blocks, sw, gamma, normed, nb, snapshot, B, eps, NULL, NULL);
+}
+
+/* kern_k3_land_add2_bf16 (k3_land_bf16.cu:84-140): K1c with bf16 partials,
+ * hidden = bf16(f32(prefix2) + f32(p1) [+ f32(p2)]), left to right. */
+void k3o_land_add2_bf16(const uint16_t* p1, const uint16_t* p2, const uint16_t* prefix2,
+                        uint16_t* hidden, int two, int B) {
+#pragma omp parallel for schedule(static)
+  for (int b = 0; b < B; ++b)
+    for (int i = 0; i < H; ++i) {
+      const size_t o = (size_t)b * H + i;
+      float x = k3o_bf2f(prefix2[o]) + k3o_bf2f(p1[o]);
+      if (two) x += k3o_bf2f(p2[o]);
+      hidden[o] = k3o_f2bf(x);
+    }
 }
 
 /* K1c kern_k3_land_add2 (k3_residual_v2.cu:349-392). */

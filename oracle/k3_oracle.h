@@ -53,6 +53,18 @@ void k3o_attnres_rms(const uint16_t* prefix, uint16_t* blocks, const float* sw,
                      float eps);
 void k3o_land_add2(const float* p1, const float* p2, const uint16_t* prefix2, uint16_t* hidden,
                    int two, int B);
+/* statistics hand-off res_in -> res_mlp (k3_residual_push_stats.cu,
+ * k3_residual_nb_stats.cu); stats are [B, 8, 2] f32 */
+void k3o_attnres_rms_stats(const uint16_t* prefix, uint16_t* blocks, const float* sw,
+                           const uint16_t* gamma, uint16_t* normed, int nb, int snapshot, int B,
+                           float eps, const float* sw_mlp, float* stats);
+void k3o_land_add_attnres_rms_stats(const uint16_t* partial_bf16, const float* partial_f32,
+                                    const uint16_t* prefix, const uint16_t* blocks,
+                                    const float* sw, const uint16_t* gamma, uint16_t* prefix2,
+                                    uint16_t* normed, int nb, int snapshot, int B, float eps,
+                                    const float* stats, int nb_stats);
+void k3o_land_add2_bf16(const uint16_t* p1, const uint16_t* p2, const uint16_t* prefix2,
+                        uint16_t* hidden, int two, int B);
 
 /* ---- MXFP8 (k3_moe_prefill_v4.cu:111-140) and the fused op ------------- */
 void k3o_moe_quant(const uint16_t* x, uint8_t* q, uint8_t* sf, int rows, int cols);
@@ -105,6 +117,16 @@ void k3o_mla_prep(const float* partial_f32, const uint16_t* partial_bf16, int ml
 void k3o_mla_rope_pack(const uint16_t* latent, const uint16_t* k_rope, const uint16_t* q,
                        const uint16_t* gamma_kv, const long long* positions, uint16_t* latent_out,
                        uint16_t* q_out, float theta, float eps, int T, int H);
+
+/* ---- landing kernels (k3_land.cu, k3_land_bf16.cu, k3_situ_bf16.cu, k3_land_fused.cu) */
+void k3o_rms(const uint16_t* x, const uint16_t* gamma, uint16_t* o, int h, int B);
+void k3o_land(const float* p, uint16_t* o, int n, int off, int ldc, int B);
+float k3o_situ(float g, float u);
+void k3o_situ_n(const float* g, const float* u, float* y, size_t n);
+/* exactly one of p_f32 / p_bf16 is non-null */
+void k3o_land_situ(const float* p_f32, const uint16_t* p_bf16, uint16_t* act, int n, int B);
+void k3o_situ_rms(const uint16_t* sp, uint16_t* act, const uint16_t* lat, const uint16_t* gam,
+                  uint16_t* ln, int n, int B, int h, int L, int tokens);
 
 int k3o_num_threads(void);
 

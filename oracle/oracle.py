@@ -41,6 +41,8 @@ def lib() -> ctypes.CDLL:
         _lib.k3o_mx_exp.restype = ctypes.c_int
         _lib.k3o_mx_exp.argtypes = [ctypes.c_float]
         _lib.k3o_num_threads.restype = ctypes.c_int
+        _lib.k3o_situ.restype = ctypes.c_float
+        _lib.k3o_situ.argtypes = [ctypes.c_float, ctypes.c_float]
     return _lib
 
 
@@ -115,6 +117,38 @@ def land_add2(p1, p2, prefix2, two, B):
     hidden = np.empty((B, H), np.uint16)
     lib().k3o_land_add2(_p(p1), _p(p2), _p(prefix2), _p(hidden), two, B)
     return hidden
+
+
+def land_add2_bf16(p1, p2, prefix2, two, B):
+    """kern_k3_land_add2_bf16: bf16 partials (uint16)."""
+    hidden = np.empty((B, H), np.uint16)
+    lib().k3o_land_add2_bf16(_p(p1), _p(p2), _p(prefix2), _p(hidden), two, B)
+    return hidden
+
+
+def attnres_rms_stats(prefix, blocks, sw, gamma, nb, snapshot, B, sw_mlp=None, eps=1e-5):
+    """res_in of the push family: returns (blocks_out, normed, stats [B, 8, 2] or None)."""
+    blocks_out = None if blocks is None else blocks.copy()
+    normed = np.empty((B, H), np.uint16)
+    stats = None if sw_mlp is None else np.zeros((B, 8, 2), np.float32)
+    lib().k3o_attnres_rms_stats(_p(prefix), _p(blocks_out), _p(sw), _p(gamma), _p(normed), nb,
+                                snapshot, B, ctypes.c_float(eps),
+                                None if sw_mlp is None else _p(np.ascontiguousarray(sw_mlp, np.float32)),
+                                _p(stats))
+    return blocks_out, normed, stats
+
+
+def land_add_attnres_rms_stats(partial, prefix, blocks, sw, gamma, nb, snapshot, B, stats,
+                               nb_stats, eps=1e-5):
+    """res_mlp with res_in's candidate statistics; returns (prefix2, normed)."""
+    prefix2 = np.empty((B, H), np.uint16)
+    normed = np.empty((B, H), np.uint16)
+    bf = partial.dtype == np.uint16
+    lib().k3o_land_add_attnres_rms_stats(
+        _p(partial) if bf else None, None if bf else _p(partial), _p(prefix), _p(blocks), _p(sw),
+        _p(gamma), _p(prefix2), _p(normed), nb, snapshot, B, ctypes.c_float(eps),
+        None if stats is None else _p(np.ascontiguousarray(stats, np.float32)), nb_stats)
+    return prefix2, normed
 
 
 # ---------------------------------------------------------------- MXFP8
@@ -289,3 +323,43 @@ def mla_rope_pack(latent, k_rope, q, gamma_kv, positions, T, H, theta=50000.0, e
                             _p(np.ascontiguousarray(positions, np.int64)), _p(lat), _p(qo),
                             ctypes.c_float(theta), ctypes.c_float(eps), T, H)
     return lat, qo
+
+
+# ---------------------------------------------------------------- landing kernels
+def rms(x, gamma, h, B):
+    o = np.zeros((B, h), np.uint16)
+    lib().k3o_rms(_p(np.ascontiguousarray(x)), _p(np.ascontiguousarray(gamma)), _p(o), h, B)
+    return o
+
+
+def land(p, n, off, ldc, B):
+    o = np.empty((B, n), np.uint16)
+    lib().k3o_land(_p(np.ascontiguousarray(p, np.float32)), _p(o), n, off, ldc, B)
+    return o
+
+
+def situ(g, u):
+    """Exact SiTU of f32 operands (elementwise), as the f32 value that lands."""
+    g = np.ascontiguousarray(g, np.float32)
+    u = np.ascontiguousarray(u, np.float32)
+    y = np.empty_like(g)
+    lib().k3o_situ_n(_p(g), _p(u), _p(y), ctypes.c_size_t(g.size))
+    return y
+
+
+def land_situ(p, n, B):
+    """p float32 or uint16 (bf16) [B, 2n] -> act [B, n] bf16."""
+    act = np.empty((B, n), np.uint16)
+    p = np.ascontiguousarray(p)
+    f32 = p.dtype == np.float32
+    lib().k3o_land_situ(_p(p) if f32 else None, None if f32 else _p(p), _p(act), n, B)
+    return act
+
+
+def situ_rms(sp, lat, gam, n, B, h, L, tokens, act_in=None, ln_in=None):
+    """kern_k3_situ_rms_bf16: returns (act, ln); rows outside the grid keep act_in / ln_in."""
+    act = np.zeros((B, n), np.uint16) if act_in is None else np.array(act_in, np.uint16)
+    ln = np.zeros((L, h), np.uint16) if ln_in is None else np.array(ln_in, np.uint16)
+    lib().k3o_situ_rms(_p(np.ascontiguousarray(sp)), _p(act), _p(np.ascontiguousarray(lat)),
+                       _p(np.ascontiguousarray(gam)), _p(ln), n, B, h, L, tokens)
+    return act, ln

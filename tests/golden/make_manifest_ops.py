@@ -15,9 +15,13 @@ HOT = {
         "land_add_attnres_rms_bf16_v2_nb1", "quant_fp8_tensor", "moe_quant", "moe_route_count",
         "moe_route_tables", "moe_route_scatter", "moe_finalize", "router_topk", "mla_prep",
         "span_gather_v2", "kda_out_gate_v2",
+        # residual push family and landing kernels
+        "attnres_rms_push_first_v3", "attnres_rms_push_add2", "land_add_attnres_rms_bf16_v2_nb4",
+        "land_add_attnres_rms_bf16_v2_nb8", "land_situ_n33792", "land_situ_rms",
     ],
     "k3-tp4-prefill-16k-l0-bf16.json": [
         "attnres_rms_v2", "land_add_attnres_rms_bf16_v2", "land_add2_v2",
+        "rms", "land_n3584", "land_situ_n6144", ("land_situ_n33792", "l0_land_situ_n33792"),
     ],
 }
 
@@ -28,7 +32,8 @@ def main():
         with open(os.path.join(REF, fn)) as f:
             m = json.load(f)
         for op in ops:
-            out[op] = {"manifest": fn, **m["ops"][op]}
+            name, key = op if isinstance(op, tuple) else (op, op)
+            out[key] = {"manifest": fn, **m["ops"][name]}
         out.setdefault("_vars", m["vars"])
     with open(OUT, "w") as f:
         json.dump(out, f, indent=1, sort_keys=True)
