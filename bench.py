@@ -147,6 +147,7 @@ def bench_ops(ctx, reps: int, out_path: str | None) -> list:
         us, p10, p90 = t
         gbs = nbytes / (us * 1e-6) / 1e9
         rows.append({"op": op, "kernel": kernel, "shape": shape, "bytes": int(nbytes),
+                     "launches": 5 + reps,
                      "us": round(us, 2), "us_p10": round(p10, 2), "us_p90": round(p90, 2),
                      "gbs": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1),
                      "note": note})
@@ -263,10 +264,78 @@ def bench_ops(ctx, reps: int, out_path: str | None) -> list:
     add("weighted finalize (cfg 5d)", "kern_k3_moe_finalize", f"T={T} cols={H}",
         live * H * 2 + 2 * T * 8 * 4 + T * H * 2,
         timed(lambda: ctx.moe_finalize(fc2, e2p, wts, out, T, H, topk=8, stream=s)))
+    del fc2, out
+    bench_push_land(ctx, add, timed, bf, g, s)
     if out_path:
         with open(out_path, "w") as f:
             json.dump(rows, f, indent=1)
     return rows
+
+
+def bench_push_land(ctx, add, timed, bf, g, s) -> None:
+    """The residual push family and the landing kernels at one TP rank's share of
+    the 16k prefill (B = tokens / 4 = 4096 rows; manifest shapes).  On one GPU
+    the four ranks' normed_all buffers are local, so every normed copy is an HBM
+    write here (three of the four cross xGMI on a 4-GPU node)."""
+    import torch
+    B, HH = 4096, H
+    row = B * HH * 2
+    gm = bf(HH, mean=1.0, std=0.1)
+    sw = torch.randn(HH, generator=g, device="cuda") * 0.05
+    sw_mlp = torch.randn(HH, generator=g, device="cuda") * 0.05
+    prefix = bf(B, HH)
+    blocks = bf(B, 8, HH)
+    normed = [torch.empty((4 * B, HH), dtype=torch.bfloat16, device="cuda") for _ in range(4)]
+    peer = torch.tensor([t.data_ptr() for t in normed], dtype=torch.int64, device="cuda")
+    add("residual push v3 (res_in, nb 0, 4 ranks)", "kern_k3_attnres_rms_push", f"B={B} nb=0",
+        row + HH * 2 + row + 4 * row,
+        timed(lambda: ctx.attnres_rms_push(prefix, blocks, sw, gm, normed[1], peer, 0, 1, B, 1, 4,
+                                           version=3, stream=s)))
+    nb = 4
+    p1, p2, prefix2 = bf(B, HH), bf(B, HH), bf(B, HH)
+    hidden = torch.empty_like(p1)
+    stats = torch.empty((B, 8, 2), dtype=torch.float32, device="cuda")
+    add("residual push_add2 (res_in, nb 4, 4 ranks)", "kern_k3_attnres_rms_push",
+        f"B={B} nb={nb} two=1", 3 * row + nb * row + 2 * HH * 4 + HH * 2 + row + row + 4 * row + B * nb * 8,
+        timed(lambda: ctx.attnres_rms_push_add2(blocks, sw, gm, normed[0], peer, nb, 1, B, 0, 4,
+                                                sw_mlp, stats, p1, p2, prefix2, hidden, 1, stream=s)))
+    part = bf(B, HH)
+    pre2, nrm = torch.empty_like(part), torch.empty_like(part)
+    add("res_mlp nb 5 with res_in statistics (nb_stats 4)", "kern_k3_land_add_attnres_rms_nb5",
+        f"B={B} nb=5", 2 * row + 5 * row + HH * 4 + HH * 2 + 2 * row + B * 4 * 8,
+        timed(lambda: ctx.land_add_attnres_rms_nb_stats(part, prefix, blocks, sw_mlp, gm, pre2, nrm,
+                                                        5, 0, B, stats, 4, stream=s)))
+    del normed, peer, p1, p2, prefix2, hidden, part, pre2, nrm, blocks, prefix
+    # landing kernels (k3_land / k3_situ_bf16 / k3_land_fused)
+    h = 3584
+    lat = bf(B, h)
+    gl = bf(h, mean=1.0, std=0.1)
+    ln = torch.empty_like(lat)
+    add("rms (l0, h 3584)", "kern_k3_rms", f"B={B} h={h}", 2 * B * h * 2 + h * 2,
+        timed(lambda: ctx.rms(lat, gl, ln, h, B, stream=s)))
+    pf = torch.randn((B, h), generator=g, device="cuda")
+    lo = torch.empty((B, h), dtype=torch.bfloat16, device="cuda")
+    add("land (l0, n 3584)", "kern_k3_land", f"B={B} n={h}", B * h * 4 + B * h * 2,
+        timed(lambda: ctx.land(pf, lo, h, 0, h, B, stream=s)))
+    del pf, lo
+    for n, kind in ((33792, "f32"), (6144, "f32"), (33792, "situ_bf16")):
+        if kind == "f32":
+            p = torch.randn((B, 2 * n), generator=g, device="cuda") * 3.0
+            nm, ker, ib = f"SiTU landing f32 (n {n})", "kern_k3_land_situ", 4
+        else:
+            p = bf(B, 2 * n, std=3.0)
+            nm, ker, ib = f"SiTU landing bf16 (l0, n {n})", "kern_k3_situ_bf16", 2
+        act = torch.empty((B, n), dtype=torch.bfloat16, device="cuda")
+        add(nm, ker, f"B={B} n={n}", B * 2 * n * ib + B * n * 2,
+            timed(lambda: ctx.land_situ(p, act, n, B, variant="situ_bf16" if kind != "f32" else None,
+                                        stream=s)))
+        del p, act
+    n = 6144
+    sp = bf(B, 2 * n, std=2.0)
+    act = torch.empty((B, n), dtype=torch.bfloat16, device="cuda")
+    add("SiTU landing + latent rms (fused)", "kern_k3_situ_rms_bf16", f"B=L={B} n={n} h={h}",
+        B * 2 * n * 2 + B * n * 2 + 2 * B * h * 2 + h * 2,
+        timed(lambda: ctx.situ_rms(sp, act, lat, gl, ln, n, B, h, B, 4 * B, stream=s)))
 
 
 # Per-op kernels, in launch order, for the counter table (kernel names as the
@@ -286,6 +355,15 @@ OP_KERNELS = {
                                                  "kern_k3_moe_route_scatter"],
     "MXFP8 permute (cfg 5c)": ["k3h_moe_permute_mx"],
     "weighted finalize (cfg 5d)": ["kern_k3_moe_finalize"],
+    "residual push v3 (res_in, nb 0, 4 ranks)": ["kern_k3_attnres_rms_push"],
+    "residual push_add2 (res_in, nb 4, 4 ranks)": ["kern_k3_attnres_rms_push"],
+    "res_mlp nb 5 with res_in statistics (nb_stats 4)": ["kern_k3_land_add_attnres_rms_nb5"],
+    "rms (l0, h 3584)": ["kern_k3_rms"],
+    "land (l0, n 3584)": ["kern_k3_land"],
+    "SiTU landing f32 (n 33792)": ["kern_k3_land_situ"],
+    "SiTU landing f32 (n 6144)": ["kern_k3_land_situ"],
+    "SiTU landing bf16 (l0, n 33792)": ["kern_k3_situ_bf16"],
+    "SiTU landing + latent rms (fused)": ["kern_k3_situ_rms_bf16"],
 }
 
 
@@ -303,16 +381,32 @@ def _col(row: dict, *names: str) -> str:
     raise KeyError(f"none of {names} in {sorted(row)}")
 
 
-def counter_medians(csv_path: str, counter: str) -> dict:
-    """Per kernel name: median over dispatches of `counter` (KiB per dispatch)
-    from a rocprofv3 --pmc CSV (counter_collection.csv)."""
+def counter_values(csv_path: str, counter: str) -> dict:
+    """Per kernel name: `counter` (KiB per dispatch) of every dispatch, in
+    dispatch order, from a rocprofv3 --pmc CSV (counter_collection.csv)."""
     per = {}
     for r in _csv_rows(csv_path):
         if _col(r, "Counter_Name") != counter:
             continue
         name = _col(r, "Kernel_Name").split("(")[0].strip()
-        per.setdefault(name, []).append(float(_col(r, "Counter_Value")))
-    return {k: sorted(v)[len(v) // 2] for k, v in per.items()}
+        per.setdefault(name, []).append((int(_col(r, "Dispatch_Id")), float(_col(r, "Counter_Value"))))
+    return {k: [v for _, v in sorted(d)] for k, d in per.items()}
+
+
+class _Dispatches:
+    """Hands out each op's dispatches of a kernel in launch order (ops that share
+    an entry name, e.g. the push modules, take consecutive runs)."""
+
+    def __init__(self, values: dict):
+        self.values, self.pos = values, {k: 0 for k in values}
+
+    def median(self, kernel: str, n: int):
+        if kernel not in self.values:
+            return None
+        i = self.pos[kernel]
+        run = self.values[kernel][i:i + n]
+        self.pos[kernel] = i + n
+        return sorted(run)[len(run) // 2] if run else None
 
 
 def traffic_table(fetch_csv: str, write_csv: str, ops_json: str) -> str:
@@ -320,20 +414,28 @@ def traffic_table(fetch_csv: str, write_csv: str, ops_json: str) -> str:
     (KiB per dispatch, median), each scaled by the factor that maps the same
     counter of k3h_stream_copy onto its known byte count, against the op's
     algorithmic bytes (from a bench.py --ops-out JSON of the same shapes)."""
-    fetch, write = counter_medians(fetch_csv, "FETCH_SIZE"), counter_medians(write_csv, "WRITE_SIZE")
+    fv, wv = counter_values(fetch_csv, "FETCH_SIZE"), counter_values(write_csv, "WRITE_SIZE")
+    fetch, write = _Dispatches(fv), _Dispatches(wv)
     ops = {r["op"]: r for r in json.load(open(ops_json))}
     copy_bytes = ops["stream copy (ceiling)"]["bytes"] // 2  # read once, written once
-    kf = copy_bytes / (fetch["k3h_stream_copy"] * 1024)
-    kw = copy_bytes / (write["k3h_stream_copy"] * 1024)
+    n_copy = ops["stream copy (ceiling)"].get("launches", len(fv["k3h_stream_copy"]))
+    kf = copy_bytes / (fetch.median("k3h_stream_copy", n_copy) * 1024)
+    kw = copy_bytes / (write.median("k3h_stream_copy", n_copy) * 1024)
+    fetch, write = _Dispatches(fv), _Dispatches(wv)
     out = [f"Scale factors from k3h_stream_copy ({copy_bytes:,} B read and written): "
            f"FETCH_SIZE x {kf:.5f}, WRITE_SIZE x {kw:.5f}", "",
            "| op | kernels | read B | written B | measured B | algorithmic B | measured / algorithmic |",
            "|---|---|---:|---:|---:|---:|---:|"]
     for op, kernels in OP_KERNELS.items():
-        if op not in ops or any(k not in fetch or k not in write for k in kernels):
+        if op not in ops:
             continue
-        rd = sum(fetch[k] for k in kernels) * 1024 * kf
-        wr = sum(write[k] for k in kernels) * 1024 * kw
+        n = ops[op].get("launches", 0)
+        f = [fetch.median(k, n) for k in kernels]
+        w = [write.median(k, n) for k in kernels]
+        if None in f or None in w:
+            continue
+        rd = sum(f) * 1024 * kf
+        wr = sum(w) * 1024 * kw
         alg = ops[op]["bytes"]
         out.append(f"| {op} | {', '.join('`%s`' % k for k in kernels)} | {rd:,.0f} | {wr:,.0f} | "
                    f"{rd + wr:,.0f} | {alg:,} | {(rd + wr) / alg:.3f} |")

@@ -135,12 +135,17 @@ K3H_API int k3h_land_add2_bf16(k3h_ctx_t ctx, void* stream, const void* p1, cons
                                const void* prefix2, void* hidden, int two, int B);
 
 /* ---- landing kernels (shared-expert MLP, MoE latent norm) -------------------
+ * The entries run under the manifests' grids; these typed calls launch compact
+ * grids of 256-thread blocks sized to the work where the shape allows (the
+ * manifest grids' idle waves cost more than the work on MI355X).
  * kern_k3_rms (k3_land.cu:104; l0-bf16 op rms, json:399525): o = bf16(x * r) (x)
- * gamma, r = 1/sqrt(sum x^2 / h + 1e-5); x, o [B, h] bf16.  grid (B), block 1024. */
+ * gamma, r = 1/sqrt(sum x^2 / h + 1e-5); x, o [B, h] bf16.  Manifest grid (B),
+ * block 1024; typed call ceil(B/4) x 256 when h % 8 == 0 and h <= 8192. */
 K3H_API int k3h_rms(k3h_ctx_t ctx, void* stream, const void* x, const void* gamma, void* o, int h,
                     int B);
 /* kern_k3_land (k3_land.cu:168; l0-bf16 op land_n3584, json:400710):
- * o[b, i] = bf16(p[b*ldc + off + i]), i < n.  grid (B, ceil(n/1024)), block 1024. */
+ * o[b, i] = bf16(p[b*ldc + off + i]), i < n.  Manifest grid (B, ceil(n/1024)),
+ * block 1024; typed call ceil(B*n/2048) x 256 when (n | off | ldc) % 4 == 0. */
 K3H_API int k3h_land(k3h_ctx_t ctx, void* stream, const float* p, void* o, int n, int off, int ldc,
                      int B);
 /* SiTU landing act[b, i] = bf16(4 tanh(g/4) sigmoid(g) * 25 tanh(u/25)), gate g and
@@ -150,7 +155,8 @@ K3H_API int k3h_land(k3h_ctx_t ctx, void* stream, const float* p, void* o, int n
  *   1  kern_k3_land_situ_bf16, p bf16 (k3_land_bf16.cu:56; module k3_land_bf16);
  *   2  kern_k3_situ_bf16, p bf16 (k3_situ_bf16.cu:9; l0 op land_situ_n33792,
  *      json:400660).
- * grid (B, ceil(n/1024)), block 1024. */
+ * Manifest grid (B, ceil(n/1024)), block 1024; typed call ceil(B*n/2048) x 256
+ * when n % 8 == 0. */
 K3H_API int k3h_land_situ(k3h_ctx_t ctx, void* stream, int bf16_in, const void* p, void* act,
                           int n, int B);
 /* kern_k3_situ_rms_bf16 (k3_land_fused.cu:151; op land_situ_rms, json:406727): the

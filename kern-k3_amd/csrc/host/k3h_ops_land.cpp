@@ -1,13 +1,18 @@
 // Typed wrappers: landing kernels of the shared-expert MLP and the MoE latent
-// RMSNorm.  Grids are the manifests': land_situ_n33792 (k3-tp4-prefill-16k.json:
+// RMSNorm.  The manifests launch land_situ_n33792 (k3-tp4-prefill-16k.json:
 // 405746) and the l0-bf16 ops rms (399525), land_n3584 (400710),
-// land_situ_n6144 (400768), land_situ_n33792 (400660, k3_situ_bf16): grid
-// (rows, ceil(n / 1024)) of 1024 threads; land_situ_rms (406727): grid
-// 3 ceil(tokens / 16) of 512 threads.
+// land_situ_n6144 (400768) and land_situ_n33792 (400660, k3_situ_bf16) on a
+// grid (rows, ceil(n / 1024)) of 1024 threads, and land_situ_rms (406727) on
+// 3 ceil(tokens / 16) blocks of 512.  The entries are correct under those grids;
+// the typed calls here launch compact grids of 256-thread blocks sized to the
+// work (the entries walk the flattened output), because on MI355X the manifest
+// grids' idle waves cost more than the work itself.  Shapes off the vector
+// paths keep the manifest grid.
 #include "k3h_internal.h"
 
 namespace {
 constexpr uint32_t kBlock = 1024;
+constexpr uint32_t kCompact = 256;
 }  // namespace
 
 extern "C" {
@@ -20,6 +25,9 @@ K3H_API int k3h_rms(k3h_ctx_t ctx, void* stream, const void* x, const void* gamm
   if (B == 0) return K3H_OK;
   K3hArgs a;
   a.ptr(x).ptr(gamma).ptr(o).i32(h).i32(B);
+  if (h % 8 == 0 && h <= 8192)  // one row per wave, 4 per workgroup
+    return k3h_run(ctx, "k3_land", "kern_k3_rms", k3h_cdiv(B, kCompact / 64), 1, 1, kCompact,
+                   stream, a);
   return k3h_run(ctx, "k3_land", "kern_k3_rms", (uint32_t)B, 1, 1, kBlock, stream, a);
 }
 
@@ -31,6 +39,9 @@ K3H_API int k3h_land(k3h_ctx_t ctx, void* stream, const float* p, void* o, int n
   if (B == 0) return K3H_OK;
   K3hArgs a;
   a.ptr(p).ptr(o).i32(n).i32(off).i32(ldc).i32(B);
+  if (vec)  // 8 values per thread
+    return k3h_run(ctx, "k3_land", "kern_k3_land", k3h_cdiv((int64_t)B * n, 8 * kCompact), 1, 1,
+                   kCompact, stream, a);
   return k3h_run(ctx, "k3_land", "kern_k3_land", (uint32_t)B, k3h_cdiv(n, kBlock), 1, kBlock,
                  stream, a);
 }
@@ -47,6 +58,9 @@ K3H_API int k3h_land_situ(k3h_ctx_t ctx, void* stream, int bf16_in, const void* 
   const char* ent = bf16_in == 0   ? "kern_k3_land_situ"
                     : bf16_in == 1 ? "kern_k3_land_situ_bf16"
                                    : "kern_k3_situ_bf16";
+  if (vec)  // 8 values per thread
+    return k3h_run(ctx, mod, ent, k3h_cdiv((int64_t)B * n, 8 * kCompact), 1, 1, kCompact, stream,
+                   a);
   return k3h_run(ctx, mod, ent, (uint32_t)B, k3h_cdiv(n, kBlock), 1, kBlock, stream, a);
 }
 

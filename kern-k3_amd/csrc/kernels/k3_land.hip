@@ -33,15 +33,19 @@
 //          (k3_land_fused.cu:1-33, 151-202).
 //
 // Work split.  Every elementwise kernel ignores the reference's per-row mapping
-// (the manifests' grids leave 3/4 of the launched threads without work at
-// n = 33792) and walks the flattened [rows, n] output instead: workgroup L (the
-// linear block id) owns 8 consecutive values per thread, i.e. elements
-// [L * 8 * blockDim, (L + 1) * 8 * blockDim); ids past the end exit.  The
-// manifest grids always cover the tensor that way.  The rms kernels give each
-// wave one row (16 rows per 1024-thread workgroup, 4 per 512-thread rms job),
-// lane l playing the reference threads l + 64 k, so no workgroup barrier is
+// and walks the flattened [rows, n] output instead: workgroup L (the linear
+// block id) owns 8 consecutive values per thread (land: two groups of 4), i.e.
+// elements [L * 8 * blockDim, (L + 1) * 8 * blockDim); ids past the end exit.
+// Any grid that covers the tensor works: the manifests' grids (one thread per
+// value, 1024-thread blocks) do, and so do the compact grids the typed k3h
+// calls launch (256-thread blocks, exactly as many as there is work) -- on
+// MI355X the empty waves of the manifest grid cost more than the work (the
+// (4096, 33) x 1024 grid of land_situ_n33792 takes 116 us to dispatch with no
+// work at all).  The rms kernels give each wave one row (blockDim / 64 rows
+// per workgroup, 4 per 512-thread rms job), lane l playing the reference
+// threads l + 64 k of its 1024-thread block, so no workgroup barrier is
 // needed; shapes outside that fast path (h % 8 != 0 or h > 8192) run the
-// reference's own layout, one row per 1024-thread workgroup.
+// reference's own layout, one row per workgroup of blockDim (1024) threads.
 //
 // SiTU numerics: tanh and the logistic are evaluated from the hardware 2^x and
 // reciprocal (v_exp_f32, v_rcp_f32), with an odd Taylor series near 0 where
@@ -192,8 +196,9 @@ K3_DEV void k3_rms_row_block(const uint16_t* __restrict__ xr, const uint16_t* __
   const int tid = threadIdx.x;
   const bool vec = (h & 7) == 0;
   float s = 0.0f;
+  const int nt = (int)blockDim.x;  // 1024 in the manifest, the order the checker replays
   if (vec) {
-    for (int u = tid; u < (h >> 3); u += 1024) {
+    for (int u = tid; u < (h >> 3); u += nt) {
       const k3_u4 x = k3_ld16(xr + 8 * u);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -203,7 +208,7 @@ K3_DEV void k3_rms_row_block(const uint16_t* __restrict__ xr, const uint16_t* __
       }
     }
   } else {
-    for (int i = tid; i < h; i += 1024) {
+    for (int i = tid; i < h; i += nt) {
       const float v = k3_bf(xr[i]);
       s = __builtin_fmaf(v, v, s);
     }
@@ -217,7 +222,7 @@ K3_DEV void k3_rms_row_block(const uint16_t* __restrict__ xr, const uint16_t* __
   for (int i = 0; i < 32; ++i) w[i] = i < nw ? s_w[i] : 0.0f;
   const float r = k3_rsqrt_cr(k3_bfly32_tree(w, nw) / (float)h + K3_RMS_EPS);
   if (vec) {
-    for (int u = tid; u < (h >> 3); u += 1024) {
+    for (int u = tid; u < (h >> 3); u += nt) {
       const k3_u4 x = k3_ld16(xr + 8 * u);
       const k3_u4 g = k3_ld16(gamma + 8 * u);
       k3_u4 o;
@@ -227,7 +232,7 @@ K3_DEV void k3_rms_row_block(const uint16_t* __restrict__ xr, const uint16_t* __
       k3_st16(orow + 8 * u, o);
     }
   } else {
-    for (int i = tid; i < h; i += 1024) {
+    for (int i = tid; i < h; i += nt) {
       const uint32_t y = k3_pack_bf2(k3_bf(xr[i]) * r, 0.0f);
       orow[i] = (uint16_t)k3_mul_bf2(y, gamma[i]);
     }
@@ -256,16 +261,17 @@ extern "C" __global__ void __launch_bounds__(1024) kern_k3_land(
   if (n <= 0 || B <= 0) return;
   const long long total = (long long)B * n;
   if (((n | off | ldc) & 3) == 0) {
-    // two 4-value groups per thread over the flattened [B, n] output
-    const long long q0 = ((long long)k3_linear_block() * blockDim.x + threadIdx.x) * 2;
+    // two 4-value groups per thread over the flattened [B, n] output, group k of
+    // the workgroup's 2 * blockDim at k * blockDim + tid (coalesced per k)
+    const long long q0 = (long long)k3_linear_block() * 2 * blockDim.x + threadIdx.x;
     const int nq = n >> 2;
     k3_u4 a[2];
     long long e[2];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-      const long long q = min(q0 + k, total / 4 - 1);
+      e[k] = q0 + (long long)k * blockDim.x;
+      const long long q = min(e[k], total / 4 - 1);
       const long long row = q / nq, c = (q - row * nq) * 4;
-      e[k] = q0 + k;
       a[k] = k3_ld16_nt(p + row * ldc + off + c);
     }
 #pragma unroll
