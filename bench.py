@@ -301,6 +301,10 @@ def bench_push_land(ctx, add, timed, bf, g, s) -> None:
                                                 sw_mlp, stats, p1, p2, prefix2, hidden, 1, stream=s)))
     part = bf(B, HH)
     pre2, nrm = torch.empty_like(part), torch.empty_like(part)
+    add("K1b nb 1 entry (manifest res_mlp)", "kern_k3_land_add_attnres_rms_nb1", f"B={B} nb=1",
+        2 * row + row + HH * 4 + HH * 2 + 2 * row,
+        timed(lambda: ctx.land_add_attnres_rms_nb(part, prefix, blocks, sw, gm, pre2, nrm, 1, 0, B,
+                                                  stream=s)))
     add("res_mlp nb 5 with res_in statistics (nb_stats 4)", "kern_k3_land_add_attnres_rms_nb5",
         f"B={B} nb=5", 2 * row + 5 * row + HH * 4 + HH * 2 + 2 * row + B * 4 * 8,
         timed(lambda: ctx.land_add_attnres_rms_nb_stats(part, prefix, blocks, sw_mlp, gm, pre2, nrm,
@@ -357,6 +361,7 @@ OP_KERNELS = {
     "weighted finalize (cfg 5d)": ["kern_k3_moe_finalize"],
     "residual push v3 (res_in, nb 0, 4 ranks)": ["kern_k3_attnres_rms_push"],
     "residual push_add2 (res_in, nb 4, 4 ranks)": ["kern_k3_attnres_rms_push"],
+    "K1b nb 1 entry (manifest res_mlp)": ["kern_k3_land_add_attnres_rms_nb1"],
     "res_mlp nb 5 with res_in statistics (nb_stats 4)": ["kern_k3_land_add_attnres_rms_nb5"],
     "rms (l0, h 3584)": ["kern_k3_rms"],
     "land (l0, n 3584)": ["kern_k3_land"],

@@ -39,27 +39,34 @@
 K3_DEV void k3_push_land_add2(const uint16_t* __restrict__ p1, const uint16_t* __restrict__ p2,
                               const uint16_t* __restrict__ prefix2, uint16_t* __restrict__ hidden,
                               int two, size_t row, int t, k3_u4* pv) {
+  // all loads first, then the adds and the hidden stores
+  k3_u4 a[K3_KVPT], e[K3_KVPT];
 #pragma unroll
   for (int v = 0; v < K3_KVPT; ++v) {
-    const size_t off = row + k3_vec_off(t, v);
-    const k3_u4 a = k3_ld16_nt(p1 + off);
-    const k3_u4 c = k3_ld16_nt(prefix2 + off);
-    k3_u4 e = {0u, 0u, 0u, 0u};
-    if (two) e = k3_ld16_nt(p2 + off);
+    a[v] = k3_ld16_nt(p1 + row + k3_vec_off(t, v));
+    pv[v] = k3_ld16_nt(prefix2 + row + k3_vec_off(t, v));
+  }
+  if (two) {
+#pragma unroll
+    for (int v = 0; v < K3_KVPT; ++v) e[v] = k3_ld16_nt(p2 + row + k3_vec_off(t, v));
+  }
+#pragma unroll
+  for (int v = 0; v < K3_KVPT; ++v) {
     k3_u4 o;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      float x = k3_bf_lo(c[j]) + k3_bf_lo(a[j]);
-      float y = k3_bf_hi(c[j]) + k3_bf_hi(a[j]);
+      float x = k3_bf_lo(pv[v][j]) + k3_bf_lo(a[v][j]);
+      float y = k3_bf_hi(pv[v][j]) + k3_bf_hi(a[v][j]);
       if (two) {
-        x += k3_bf_lo(e[j]);
-        y += k3_bf_hi(e[j]);
+        x += k3_bf_lo(e[v][j]);
+        y += k3_bf_hi(e[v][j]);
       }
       o[j] = k3_pack_bf2(x, y);
     }
     pv[v] = o;
-    k3_st16(hidden + off, o);
   }
+#pragma unroll
+  for (int v = 0; v < K3_KVPT; ++v) k3_st16(hidden + row + k3_vec_off(t, v), pv[v]);
 }
 #endif
 
