@@ -89,6 +89,17 @@ K3_DEV float k3_row_rscale(float tot, float eps) {
 #define K3_MIX_STATS_OUT 1
 #define K3_MIX_STATS_IN 2
 
+// Zero that the compiler cannot see through, computed after `dep`.  Added to
+// the addresses of a vector step's loads, it keeps them from being issued
+// before the value they are made to wait for (with straight-line code the
+// compiler otherwise hoists every step's loads to the top of the pass) and from
+// being merged with identical loads of an earlier pass.
+K3_DEV int k3_zero_after(float dep) {
+  int z = 0;
+  asm volatile("" : "+v"(z) : "v"(dep));
+  return z;
+}
+
 template <int NBC, int MODE = 0>
 K3_DEV void k3_attnres_mix(const uint16_t* __restrict__ blk_row, k3_u4* pv,
                            const float* __restrict__ sw, int nb_rt, float eps, int t,
@@ -105,11 +116,25 @@ K3_DEV void k3_attnres_mix(const uint16_t* __restrict__ blk_row, k3_u4* pv,
   const int lane32 = t & 31, hw = t >> 5;
 
   // pass 1: sum x^2 and sum x * sw per candidate (prefix kept at index K3_NB_MAX).
-  // A vector step's loads (candidates, sw, sw_mlp) all go out before any use;
-  // with a compile-time nb the next step's loads also go out before this step's
-  // arithmetic (PF: the vector memory counter retires in issue order, so the
-  // loads of a step are issued together and waited for together).
-  constexpr int PF = NBC >= 0 ? 1 : 0;
+  // A vector step's loads (candidates, sw, sw_mlp) all go out before any use,
+  // and the next step's loads go out before this step's arithmetic (the vector
+  // memory counter retires in issue order, so a step's loads are issued
+  // together and waited for together).
+  // With one or two candidates (compile-time nb) the candidate rows stay in
+  // registers from pass 1 to pass 2 (RES): all their loads go out first and
+  // pass 2 reads nothing.
+  // PF: vector steps whose loads are in flight beyond the current one (deeper
+  // prefetch measured no faster: at nb >= 3 the time goes to pass 2 re-reading
+  // candidates that no longer are in the 4 MB per-XCD L2).
+  constexpr int PF = 1;
+  constexpr bool RES = NBC >= 1 && NBC <= 2;
+  k3_u4 xr[RES ? NBC : 1][K3_KVPT];
+  if constexpr (RES) {
+#pragma unroll
+    for (int c = 0; c < NBC; ++c)
+#pragma unroll
+      for (int v = 0; v < K3_KVPT; ++v) xr[c][v] = k3_ld16(blk_row + (size_t)c * K3_H + k3_vec_off(t, v));
+  }
   float sq[K3_NB_MAX + 1], dp[K3_NB_MAX + 1], dm[K3_NB_MAX];
 #pragma unroll
   for (int c = 0; c <= K3_NB_MAX; ++c) { sq[c] = 0.0f; dp[c] = 0.0f; }
@@ -117,11 +142,11 @@ K3_DEV void k3_attnres_mix(const uint16_t* __restrict__ blk_row, k3_u4* pv,
   for (int c = 0; c < K3_NB_MAX; ++c) dm[c] = 0.0f;
   k3_u4 xb[PF + 1][K3_NB_MAX];
   float4 wb[PF + 1][SOUT ? 4 : 2];
-  auto load1 = [&](int v, int slot) {
-    const int u = k3_vec_off(t, v);
+  auto load1 = [&](int v, int slot, float dep) {
+    const int u = k3_vec_off(t, v) + k3_zero_after(dep);
 #pragma unroll
     for (int c = 0; c < K3_NB_MAX; ++c) {
-      if (c >= nb) break;
+      if (RES || c >= nb) break;
       if (SIN && c < ns) continue;
       xb[slot][c] = k3_ld16(blk_row + (size_t)c * K3_H + u);
     }
@@ -132,12 +157,21 @@ K3_DEV void k3_attnres_mix(const uint16_t* __restrict__ blk_row, k3_u4* pv,
       wb[slot][SOUT ? 3 : 1] = *(const float4*)(sw_mlp + u + 4);
     }
   };
-  if (PF) load1(0, 0);
+#pragma unroll
+  for (int d = 0; d < PF; ++d) load1(d, d, __uint_as_float(pv[0][0]));
 #pragma unroll
   for (int v = 0; v < K3_KVPT; ++v) {
-    const int slot = PF ? (v & 1) : 0;
-    if (!PF) load1(v, 0);
-    else if (v + 1 < K3_KVPT) load1(v + 1, (v + 1) & 1);
+    const int slot = v % (PF + 1);
+    // the loads of step v + 1 wait for every sum of step v - 1: two steps in
+    // flight at most
+    float dep = dp[K3_NB_MAX];
+#pragma unroll
+    for (int c = 0; c < K3_NB_MAX; ++c) {
+      if (c >= nb) break;
+      dep += sq[c] + dp[c];
+      if (SOUT) dep += dm[c];
+    }
+    if (v + PF < K3_KVPT) load1(v + PF, (v + PF) % (PF + 1), dep);
     const float4 a = wb[slot][0], b = wb[slot][1];
     const float swv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
     float swm[8];
@@ -158,7 +192,9 @@ K3_DEV void k3_attnres_mix(const uint16_t* __restrict__ blk_row, k3_u4* pv,
     for (int c = 0; c < K3_NB_MAX; ++c) {
       if (c >= nb) break;
       if (SIN && c < ns) continue;
-      const k3_u4 x = xb[slot][c];
+      k3_u4 x;
+      if constexpr (RES) x = xr[c][v];
+      else x = xb[slot][c];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const float lo = k3_bf_lo(x[j]), hi = k3_bf_hi(x[j]);
@@ -230,21 +266,28 @@ K3_DEV void k3_attnres_mix(const uint16_t* __restrict__ blk_row, k3_u4* pv,
   for (int c = 0; c < K3_NB_MAX; ++c) p[c] = __shfl(pmine, base + c, 64);
   const float pp = __shfl(pmine, base + nb, 64);
 
-  // pass 2: f32 mix, one bf16 landing per value (loads issued as in pass 1)
-  auto load2 = [&](int v, int slot) {
-    const int u = k3_vec_off(t, v);
+  // pass 2: f32 mix, one bf16 landing per value (loads issued as in pass 1).
+  // The row base goes through an empty asm so that the compiler re-loads the
+  // candidates here instead of keeping every pass-1 value live across the
+  // softmax (7 nb vectors per thread: more registers than a wave has at nb >= 3).
+  auto load2 = [&](int v, int slot, float dep) {
+    const int u = k3_vec_off(t, v) + k3_zero_after(dep);
 #pragma unroll
     for (int c = 0; c < K3_NB_MAX; ++c) {
-      if (c >= nb) break;
+      if (RES || c >= nb) break;
       xb[slot][c] = k3_ld16(blk_row + (size_t)c * K3_H + u);
     }
   };
-  if (PF) load2(0, 0);
+  // Pass 2 walks the vectors last-read-first: the candidates pass 1 touched last
+  // are the likeliest still in L2 (each value's sum is independent of v).
+  float dep2 = pp;
 #pragma unroll
-  for (int v = 0; v < K3_KVPT; ++v) {
-    const int slot = PF ? (v & 1) : 0;
-    if (!PF) load2(v, 0);
-    else if (v + 1 < K3_KVPT) load2(v + 1, (v + 1) & 1);
+  for (int d = 0; d < PF; ++d) load2(K3_KVPT - 1 - d, d, dep2);
+#pragma unroll
+  for (int w = 0; w < K3_KVPT; ++w) {
+    const int v = K3_KVPT - 1 - w;
+    const int slot = w % (PF + 1);
+    if (w + PF < K3_KVPT) load2(v - PF, (w + PF) % (PF + 1), dep2);
     const k3_u4* xv = xb[slot];
     float acc[8];
 #pragma unroll
@@ -255,7 +298,9 @@ K3_DEV void k3_attnres_mix(const uint16_t* __restrict__ blk_row, k3_u4* pv,
 #pragma unroll
     for (int c = 0; c < K3_NB_MAX; ++c) {
       if (c >= nb) break;
-      const k3_u4 x = xv[c];
+      k3_u4 x;
+      if constexpr (RES) x = xr[c][v];
+      else x = xv[c];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         acc[2 * j] = __builtin_fmaf(p[c], k3_bf_lo(x[j]), acc[2 * j]);
@@ -264,6 +309,7 @@ K3_DEV void k3_attnres_mix(const uint16_t* __restrict__ blk_row, k3_u4* pv,
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) pv[v][j] = k3_pack_bf2(acc[2 * j], acc[2 * j + 1]);
+    dep2 = __uint_as_float(pv[v][0] ^ pv[v][1] ^ pv[v][2] ^ pv[v][3]);
   }
 }
 
