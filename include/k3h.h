@@ -279,6 +279,56 @@ K3H_API int k3h_mla_rope_pack(k3h_ctx_t ctx, void* stream, const void* latent,
                               const long long* positions, void* latent_out, void* q_out,
                               float theta, float eps, int T, int H);
 
+/* ---- MoE expert GEMMs (MX-scaled matrix cores) ---------------------------------
+ * They replace the reference's prebuilt batched GEMMs of manifest ops moe_fc1
+ * (k3-tp4-prefill-16k.json:405185; MxE4m3 x MxE2m1 -> MxE4m3 with the siTuGlu
+ * activation, kernels.toml:6-9) and moe_fc2 (json:405419; -> bf16), whose
+ * per-expert alpha / beta buffers the manifest fills with 4.0 and 25.0
+ * (load.fill_f32 calls), and the load-time layouts kern_k3_moe_w_shuffle /
+ * kern_k3_moe_sf_shuffle (k3_moe_prefill_v4.cu:69-80, 304-327).
+ *
+ * k3h_moe_w_tile: row-major e2m1 weights src [experts, n, k/2] (low nibble =
+ * even k) -> the MFMA-operand tiled layout dst (same size); gated: src rows are
+ * [up; gate] halves (n/2 each) and the tiles alternate up / gate.  n % 32 == 0
+ * (n % 64 gated), k % 64 == 0.
+ * k3h_moe_sf_tile: E8M0 scales src [experts, n, k/32] -> tiled dst (same size,
+ * 2-byte aligned).  k % 128 == 0.
+ * k3h_moe_gemm_mx: C[r, :] = a(src(r), :) . w_e^T over the route tiles t <
+ * *num_tiles (rows [128 t, 128 t + 128), expert e = cta_batch[t]); a e4m3
+ * [rows, K] (16-byte aligned rows) with E8M0 a_sf [rows, K/32]; src(r) =
+ * a_rows[r] when a_rows (route_map) is given, else r.  Epilogue:
+ *   K3H_GEMM_F32      out f32 [tiles*128, N];
+ *   K3H_GEMM_BF16     out bf16 [tiles*128, N] (fc2);
+ *   K3H_GEMM_SITU_MX  gated weights: x = bf16(situ(bf16(gate), bf16(up);
+ *                     alpha[e], beta[e])) -> out e4m3 [.., N/2], out_sf E8M0
+ *                     [.., N/64], quantised as kern_k3_moe_quant (fc1).
+ * The grid is (N/256, max_tiles); tiles >= *num_tiles exit.  N % 256 == 0,
+ * K % 128 == 0; rows of padding tiles route token 0 and are computed. */
+#define K3H_GEMM_F32 0
+#define K3H_GEMM_BF16 1
+#define K3H_GEMM_SITU_MX 2
+K3H_API int k3h_moe_w_tile(k3h_ctx_t ctx, void* stream, const void* src, void* dst, int experts,
+                           int n, int k, int gated);
+K3H_API int k3h_moe_sf_tile(k3h_ctx_t ctx, void* stream, const void* src, void* dst, int experts,
+                            int n, int k, int gated);
+K3H_API int k3h_moe_gemm_mx(k3h_ctx_t ctx, void* stream, int epilogue, const void* a,
+                            const void* a_sf, const int* a_rows, const void* wt, const void* wsf,
+                            const int* num_tiles, const int* cta_batch, int max_tiles, int E,
+                            int N, int K, void* out, void* out_sf, const float* alpha,
+                            const float* beta);
+/* moe_fc1 / moe_fc2 in the manifest ops' parameter order (json:405185 /
+ * 405419), with this build's tiled weights; total_padded and cta_limit are
+ * accepted for the signature's sake (the tile count bounds the work). */
+K3H_API int k3h_moe_fc1(k3h_ctx_t ctx, void* stream, const void* w13t, const void* w13_sft,
+                        const void* a_q, const void* a_sf, void* fc1_out, void* fc1_sf,
+                        const int* route_map, const float* alpha, const float* beta,
+                        const int* num_non_exiting, const int* total_padded, const int* cta_batch,
+                        const int* cta_limit, int max_tiles, int E, int K, int inter);
+K3H_API int k3h_moe_fc2(k3h_ctx_t ctx, void* stream, const void* w2t, const void* w2_sft,
+                        const void* fc1_out, const void* fc1_sf, void* fc2_out,
+                        const int* num_non_exiting, const int* total_padded, const int* cta_batch,
+                        const int* cta_limit, int max_tiles, int E, int inter, int cols);
+
 /* ---- measurement support --------------------------------------------------
  * k3h_stream_copy: dst[i] = src[i] for n16 16-byte vectors with non-temporal
  * loads and stores, one vector per thread (module k3h_fused).  No reference

@@ -52,6 +52,7 @@ SOURCES = {
     "k3_land_bf16": "k3_land.hip",
     "k3_situ_bf16": "k3_land.hip",
     "k3_land_fused": "k3_land.hip",
+    "k3h_moe_gemm": "k3h_moe_gemm.hip",
 }
 
 # defines implied by a base name that shares its source with another base
@@ -98,6 +99,7 @@ MODULES = [
     "k3_land_bf16",
     "k3_situ_bf16",
     "k3_land_fused",
+    "k3h_moe_gemm",
 ]
 
 DEVICE_FLAGS = [
@@ -108,7 +110,7 @@ DEVICE_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
-HOST_SOURCES = ["k3h_module.cpp", "k3h_ops_residual.cpp", "k3h_ops_push.cpp", "k3h_ops_land.cpp", "k3h_ops_quant.cpp", "k3h_ops_moe.cpp", "k3h_ops_kda.cpp", "k3h_ops_mla.cpp"]
+HOST_SOURCES = ["k3h_module.cpp", "k3h_ops_residual.cpp", "k3h_ops_push.cpp", "k3h_ops_land.cpp", "k3h_ops_gemm.cpp", "k3h_ops_quant.cpp", "k3h_ops_moe.cpp", "k3h_ops_kda.cpp", "k3h_ops_mla.cpp"]
 
 
 def module_defines(key: str) -> tuple[str, list[str]]:

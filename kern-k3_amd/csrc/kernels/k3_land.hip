@@ -53,50 +53,13 @@
 // value of the formula (the reference's tanh.approx / __expf / __frcp_rn form
 // is pinned to the same tolerance).
 #include "../common/k3_dev.h"
+#include "k3_situ.h"
 
 #ifndef K3_LAND_MODULE
 #define K3_LAND_MODULE 1
 #endif
 
 #define K3_RMS_EPS 1e-5f
-#define K3_LOG2E 0x1.715476p+0f
-
-// ---------------------------------------------------------------- SiTU math
-// tanh(y) for |y| < 0.25: y + y^3 (-1/3 + y^2 (2/15 + y^2 (-17/315 + y^2 62/2835)));
-// the first omitted term is below 2^-27 |y| there.
-K3_DEV float k3_tanh_series(float y) {
-  const float y2 = y * y;
-  float p = __builtin_fmaf(y2, 0x1.664f48p-6f, -0x1.ba1ba2p-5f);  // 62/2835, -17/315
-  p = __builtin_fmaf(p, y2, 0x1.111112p-3f);                        // 2/15
-  p = __builtin_fmaf(p, y2, -0x1.555556p-2f);                       // -1/3
-  return __builtin_fmaf(p * y2, y, y);
-}
-
-// 4 tanh(g / 4) * sigmoid(g) from t = e^(-|g| / 2):
-//   tanh(|g| / 4) = (1 - t) / (1 + t),  sigmoid(g) = 1 / (1 + t^2) (g >= 0) or
-//   t^2 / (1 + t^2) (g < 0); one reciprocal of (1 + t)(1 + t^2) serves both.
-K3_DEV float k3_situ_gate(float g) {
-  const float x = __builtin_fabsf(g);
-  const float t = __builtin_amdgcn_exp2f(x * (-0.5f * K3_LOG2E));
-  const float tt = t * t;
-  const float a = 1.0f + t, b = 1.0f + tt;
-  const float r = __builtin_amdgcn_rcpf(a * b);
-  const float th = x < 1.0f ? k3_tanh_series(x * 0.25f) : (1.0f - t) * b * r;
-  const float sg = (g >= 0.0f ? a : tt * a) * r;
-  return __builtin_copysignf(4.0f * th, g) * sg;
-}
-
-// 25 tanh(u * 0.04) (the reference scales by the f32 constant 0.04f).
-K3_DEV float k3_situ_up(float u) {
-  const float y = u * 0.04f;
-  const float x = __builtin_fabsf(y);
-  const float e = __builtin_amdgcn_exp2f(x * (-2.0f * K3_LOG2E));
-  const float th = x < 0.25f ? k3_tanh_series(x) : (1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e);
-  return 25.0f * __builtin_copysignf(th, y);
-}
-
-K3_DEV float k3_situ(float g, float u) { return k3_situ_gate(g) * k3_situ_up(u); }
-
 // Eight bf16 gate values and eight bf16 up values -> eight bf16 outputs.
 K3_DEV k3_u4 k3_situ8(k3_u4 g, k3_u4 u) {
   k3_u4 o;

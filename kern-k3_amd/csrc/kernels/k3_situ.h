@@ -1,0 +1,71 @@
+// SiTU gated activation shared by the landing kernels and the MoE fc1 epilogue:
+//   situ(g, u) = (alpha tanh(g / alpha) sigmoid(g)) * (beta tanh(u / beta))
+// with alpha = 4, beta = 25 in every K3 layer (the manifests fill the per-expert
+// moe.alpha / moe.beta buffers with 4.0 and 25.0; k3_land.cu:29-34 hard-codes
+// them with u scaled by the f32 constant 0.04f, which equals 1.0f / 25.0f).
+// tanh and the logistic come from the hardware 2^x and reciprocal (v_exp_f32,
+// v_rcp_f32), with an odd Taylor series near 0 where 1 - e^-2x would cancel.
+#pragma once
+#include "../common/k3_dev.h"
+
+#define K3_LOG2E 0x1.715476p+0f
+
+// ---------------------------------------------------------------- SiTU math
+// tanh(y) for |y| < 0.25: y + y^3 (-1/3 + y^2 (2/15 + y^2 (-17/315 + y^2 62/2835)));
+// the first omitted term is below 2^-27 |y| there.
+K3_DEV float k3_tanh_series(float y) {
+  const float y2 = y * y;
+  float p = __builtin_fmaf(y2, 0x1.664f48p-6f, -0x1.ba1ba2p-5f);  // 62/2835, -17/315
+  p = __builtin_fmaf(p, y2, 0x1.111112p-3f);                        // 2/15
+  p = __builtin_fmaf(p, y2, -0x1.555556p-2f);                       // -1/3
+  return __builtin_fmaf(p * y2, y, y);
+}
+
+// 4 tanh(g / 4) * sigmoid(g) from t = e^(-|g| / 2):
+//   tanh(|g| / 4) = (1 - t) / (1 + t),  sigmoid(g) = 1 / (1 + t^2) (g >= 0) or
+//   t^2 / (1 + t^2) (g < 0); one reciprocal of (1 + t)(1 + t^2) serves both.
+K3_DEV float k3_situ_gate(float g) {
+  const float x = __builtin_fabsf(g);
+  const float t = __builtin_amdgcn_exp2f(x * (-0.5f * K3_LOG2E));
+  const float tt = t * t;
+  const float a = 1.0f + t, b = 1.0f + tt;
+  const float r = __builtin_amdgcn_rcpf(a * b);
+  const float th = x < 1.0f ? k3_tanh_series(x * 0.25f) : (1.0f - t) * b * r;
+  const float sg = (g >= 0.0f ? a : tt * a) * r;
+  return __builtin_copysignf(4.0f * th, g) * sg;
+}
+
+// 25 tanh(u * 0.04) (the reference scales by the f32 constant 0.04f).
+K3_DEV float k3_situ_up(float u) {
+  const float y = u * 0.04f;
+  const float x = __builtin_fabsf(y);
+  const float e = __builtin_amdgcn_exp2f(x * (-2.0f * K3_LOG2E));
+  const float th = x < 0.25f ? k3_tanh_series(x) : (1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e);
+  return 25.0f * __builtin_copysignf(th, y);
+}
+
+K3_DEV float k3_situ(float g, float u) { return k3_situ_gate(g) * k3_situ_up(u); }
+
+// General alpha / beta (per expert).  inv_alpha = 1 / alpha and inv_beta =
+// 1 / beta (correctly rounded): alpha == 4 takes the shared-exponential path of
+// k3_situ_gate (identical results), beta == 25 gives inv_beta == 0.04f, so the
+// K3 constants reproduce k3_situ bit for bit.
+K3_DEV float k3_situ_gate_a(float g, float alpha, float inv_alpha) {
+  if (alpha == 4.0f) return k3_situ_gate(g);
+  const float x = __builtin_fabsf(g);
+  const float y = x * inv_alpha;
+  const float e = __builtin_amdgcn_exp2f(y * (-2.0f * K3_LOG2E));
+  const float th = y < 0.25f ? k3_tanh_series(y) : (1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e);
+  const float t2 = __builtin_amdgcn_exp2f(x * -K3_LOG2E);  // e^-|g|
+  const float r = __builtin_amdgcn_rcpf(1.0f + t2);
+  const float sg = g >= 0.0f ? r : t2 * r;
+  return __builtin_copysignf(alpha * th, g) * sg;
+}
+
+K3_DEV float k3_situ_up_b(float u, float beta, float inv_beta) {
+  const float y = u * inv_beta;
+  const float x = __builtin_fabsf(y);
+  const float e = __builtin_amdgcn_exp2f(x * (-2.0f * K3_LOG2E));
+  const float th = x < 0.25f ? k3_tanh_series(x) : (1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e);
+  return beta * __builtin_copysignf(th, y);
+}

@@ -92,6 +92,11 @@ _SIGS: dict[str, list] = {
     "k3h_land": [_P, _P, _P, _P, _I, _I, _I, _I],
     "k3h_land_situ": [_P, _P, _I, _P, _P, _I, _I],
     "k3h_situ_rms": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I],
+    "k3h_moe_w_tile": [_P, _P, _P, _P, _I, _I, _I, _I],
+    "k3h_moe_sf_tile": [_P, _P, _P, _P, _I, _I, _I, _I],
+    "k3h_moe_gemm_mx": [_P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P],
+    "k3h_moe_fc1": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I],
+    "k3h_moe_fc2": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I],
 }
 
 
@@ -565,6 +570,52 @@ class Ctx:
         _check(self.L.k3h_mla_rope_pack(self.h, _stream(stream), _ptr(latent), _ptr(k_rope), _ptr(q),
                                         _ptr(gamma_kv), _ptr(positions), _ptr(latent_out),
                                         _ptr(q_out), theta, eps, T, H), "mla_rope_pack")
+
+    # ------------------------------------------------------------ MoE expert GEMMs
+    GEMM_F32, GEMM_BF16, GEMM_SITU_MX = 0, 1, 2
+
+    def moe_w_tile(self, src, dst, experts: int, n: int, k: int, gated: int, stream=None) -> None:
+        """Row-major e2m1 weights [experts, n, k/2] -> the MFMA-operand tiled layout."""
+        nbytes = experts * n * k // 2
+        _dev(src, "src", U8, nbytes)
+        _dev(dst, "dst", U8, nbytes)
+        _check(self.L.k3h_moe_w_tile(self.h, _stream(stream), _ptr(src), _ptr(dst), experts, n, k,
+                                     gated), "moe_w_tile")
+
+    def moe_sf_tile(self, src, dst, experts: int, n: int, k: int, gated: int, stream=None) -> None:
+        """E8M0 scales [experts, n, k/32] -> the tiled scale layout."""
+        nbytes = experts * n * k // 32
+        _dev(src, "src", U8, nbytes, align=1)
+        _dev(dst, "dst", U8, nbytes, align=2)
+        _check(self.L.k3h_moe_sf_tile(self.h, _stream(stream), _ptr(src), _ptr(dst), experts, n, k,
+                                      gated), "moe_sf_tile")
+
+    def moe_gemm_mx(self, epilogue: int, a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch,
+                    max_tiles: int, E: int, N: int, K: int, out, out_sf=None, alpha=None,
+                    beta=None, stream=None) -> None:
+        """MX GEMM over the route tiles (epilogue GEMM_F32 / GEMM_BF16 / GEMM_SITU_MX)."""
+        rows = max_tiles * 128
+        _dev(a, "a", U8, K, align=16)
+        _dev(a_sf, "a_sf", U8, K // 32, align=4)
+        if a_rows is not None:
+            _dev(a_rows, "a_rows", I32, rows, align=4)
+        _dev(wt, "wt", U8, E * N * K // 2)
+        _dev(wsf, "wsf", U8, E * N * K // 32, align=2)
+        _dev(num_tiles, "num_tiles", I32, 1, align=4)
+        _dev(cta_batch, "cta_batch", I32, max_tiles, align=4)
+        if epilogue == self.GEMM_F32:
+            _dev(out, "out", F32, rows * N, align=4)
+        elif epilogue == self.GEMM_BF16:
+            _dev(out, "out", BF16, rows * N, align=2)
+        else:
+            _dev(out, "out", U8, rows * N // 2, align=1)
+            _dev(out_sf, "out_sf", U8, rows * N // 64, align=1)
+            _dev(alpha, "alpha", F32, E, align=4)
+            _dev(beta, "beta", F32, E, align=4)
+        _check(self.L.k3h_moe_gemm_mx(self.h, _stream(stream), epilogue, _ptr(a), _ptr(a_sf),
+                                      _ptr(a_rows), _ptr(wt), _ptr(wsf), _ptr(num_tiles),
+                                      _ptr(cta_batch), max_tiles, E, N, K, _ptr(out), _ptr(out_sf),
+                                      _ptr(alpha), _ptr(beta)), "moe_gemm_mx")
 
     # ------------------------------------------------------------ measurement
     def stream_copy(self, src, dst, stream=None) -> None:

@@ -130,6 +130,16 @@ void k3o_situ_rms(const uint16_t* sp, uint16_t* act, const uint16_t* lat, const 
 
 int k3o_num_threads(void);
 
+/* ---- MoE expert GEMMs (k3_oracle_gemm.c) */
+float k3o_e2m1_decode(uint8_t nib);
+void k3o_moe_gemm_mx(const uint8_t* a, const uint8_t* a_sf, const int* a_rows, const uint8_t* w,
+                     const uint8_t* w_sf, int num_tiles, const int* cta_batch, int E, int N, int K,
+                     double* out);
+void k3o_moe_gemm_mx_abs(const uint8_t* a, const uint8_t* a_sf, const int* a_rows,
+                         const uint8_t* w, const uint8_t* w_sf, int num_tiles,
+                         const int* cta_batch, int E, int N, int K, double* out);
+void k3o_situ_ab_n(const float* g, const float* u, float* y, size_t n, float alpha, float beta);
+
 #ifdef __cplusplus
 }
 #endif

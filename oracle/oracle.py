@@ -43,6 +43,8 @@ def lib() -> ctypes.CDLL:
         _lib.k3o_num_threads.restype = ctypes.c_int
         _lib.k3o_situ.restype = ctypes.c_float
         _lib.k3o_situ.argtypes = [ctypes.c_float, ctypes.c_float]
+        _lib.k3o_e2m1_decode.restype = ctypes.c_float
+        _lib.k3o_e2m1_decode.argtypes = [ctypes.c_uint8]
     return _lib
 
 
@@ -363,3 +365,52 @@ def situ_rms(sp, lat, gam, n, B, h, L, tokens, act_in=None, ln_in=None):
     lib().k3o_situ_rms(_p(np.ascontiguousarray(sp)), _p(act), _p(np.ascontiguousarray(lat)),
                        _p(np.ascontiguousarray(gam)), _p(ln), n, B, h, L, tokens)
     return act, ln
+
+
+# ---------------------------------------------------------------- MoE expert GEMMs
+def e2m1_decode(nib):
+    nib = np.asarray(nib, np.uint8)
+    f = np.vectorize(lambda v: lib().k3o_e2m1_decode(int(v)), otypes=[np.float32])
+    return f(nib)
+
+
+def moe_gemm_mx(a, a_sf, a_rows, w, w_sf, num_tiles, cta_batch, E, N, K, magnitude=False):
+    """Double-precision MX GEMM over the route tiles t < num_tiles (rows [128 t, 128 t + 128),
+    expert cta_batch[t]); rows of skipped tiles are NaN.  magnitude=True returns sum |a w|."""
+    assert K <= 8192 and K % 32 == 0 and N > 0
+    out = np.full((num_tiles * 128, N), np.nan, np.float64)
+    fn = lib().k3o_moe_gemm_mx_abs if magnitude else lib().k3o_moe_gemm_mx
+    rows = None if a_rows is None else np.ascontiguousarray(a_rows, np.int32)
+    fn(_p(np.ascontiguousarray(a, np.uint8)), _p(np.ascontiguousarray(a_sf, np.uint8)), _p(rows),
+       _p(np.ascontiguousarray(w, np.uint8)), _p(np.ascontiguousarray(w_sf, np.uint8)),
+       int(num_tiles), _p(np.ascontiguousarray(cta_batch, np.int32)), E, N, K, _p(out))
+    return out
+
+
+def situ_ab(g, u, alpha, beta):
+    """Exact gated activation of f32 operands with per-call alpha / beta (f32 value that lands)."""
+    g = np.ascontiguousarray(g, np.float32)
+    u = np.ascontiguousarray(u, np.float32)
+    y = np.empty_like(g)
+    lib().k3o_situ_ab_n(_p(g), _p(u), _p(y), ctypes.c_size_t(g.size), ctypes.c_float(alpha),
+                        ctypes.c_float(beta))
+    return y
+
+
+def moe_fc1_epilogue(c, alpha_rows, beta_rows):
+    """fc1 epilogue on f32 accumulators c [rows, N] in weight-row order ([up | gate]):
+    u = bf16(c[:, :N/2]), g = bf16(c[:, N/2:]), x = bf16(situ(g, u; alpha, beta)) per row's
+    expert, then MX quantisation of x -> (q [rows, N/2], sf [rows, N/64])."""
+    c = np.ascontiguousarray(c, np.float32)
+    rows, N = c.shape
+    half = N // 2
+    bf = lambda v: (((v.view(np.uint32).astype(np.uint64) + 0x7FFF +
+                      ((v.view(np.uint32) >> 16) & 1)) >> 16).astype(np.uint16))
+    up16, gate16 = bf(np.ascontiguousarray(c[:, :half])), bf(np.ascontiguousarray(c[:, half:]))
+    u = (up16.astype(np.uint32) << 16).view(np.float32)
+    g = (gate16.astype(np.uint32) << 16).view(np.float32)
+    x = np.empty((rows, half), np.float32)
+    for r in range(rows):
+        x[r] = situ_ab(g[r], u[r], float(alpha_rows[r]), float(beta_rows[r]))
+    x16 = bf(x)
+    return moe_quant(x16, rows, half)
