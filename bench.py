@@ -33,6 +33,9 @@ METRIC = "effective HBM GB/s (% of peak) for residual+RMSNorm+MXFP8 at 16384x716
 H = 7168
 T = 16384
 PEAK_GBS = 8000.0
+# MI355X dense MFMA peak for e4m3 operands (TFLOP/s); e4m3 x e2m1 issues at the
+# e4m3 rate (4.95 PFLOP/s measured register-to-register).
+PEAK_MX_TFLOPS = 5000.0
 
 
 def algo_bytes(rows: int) -> int:
@@ -266,6 +269,19 @@ def bench_ops(ctx, reps: int, out_path: str | None) -> list:
         timed(lambda: ctx.moe_finalize(fc2, e2p, wts, out, T, H, topk=8, stream=s)))
     del fc2, out
     bench_push_land(ctx, add, timed, bf, g, s)
+
+    def add_flop(op, kernel, shape, flops, nbytes, t, note=""):
+        us, p10, p90 = t
+        tf = flops / (us * 1e-6) / 1e12
+        rows.append({"op": op, "kernel": kernel, "shape": shape, "bytes": int(nbytes),
+                     "flops": int(flops), "bound": "mfma", "launches": 5 + reps,
+                     "us": round(us, 2), "us_p10": round(p10, 2), "us_p90": round(p90, 2),
+                     "tflops": round(tf, 1), "pct_peak": round(100 * tf / PEAK_MX_TFLOPS, 1),
+                     "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "note": note})
+        log(f"{op:42s} {us:8.2f} us (p10 {p10:7.2f}, p90 {p90:7.2f}) {tf:7.0f} TFLOP/s "
+            f"{100 * tf / PEAK_MX_TFLOPS:5.1f}% of MFMA  {note}")
+
+    bench_gemm(ctx, add_flop, timed, g, s, rmap, cb, nne, tpad, T, E)
     if out_path:
         with open(out_path, "w") as f:
             json.dump(rows, f, indent=1)
@@ -342,6 +358,52 @@ def bench_push_land(ctx, add, timed, bf, g, s) -> None:
         timed(lambda: ctx.situ_rms(sp, act, lat, gl, ln, n, B, h, B, 4 * B, stream=s)))
 
 
+def bench_gemm(ctx, add_flop, timed, g, s, rmap, cta_batch, num_tiles, tpad, T, E) -> None:
+    """The MoE expert GEMMs at the reference's shapes (latent 3584, intermediate 3072,
+    56 local experts, e2m1 weights), over the routing tables of the top-8 router run:
+    fc1 gathers its rows through route_map (SiTU-GLU + MXFP8 epilogue), fc2 reads fc1's
+    output (bf16 out).  FLOPs count the padded rows the tiles compute."""
+    import torch
+    KL, INTER, COLS = 3584, 3072, 3584
+    max_tiles = rmap.numel() // 128
+    lat = (torch.randn((T, KL), generator=g, device="cuda")).to(torch.bfloat16)
+    aq = torch.empty((T, KL), dtype=torch.uint8, device="cuda")
+    asf = torch.empty((T, KL // 32), dtype=torch.uint8, device="cuda")
+    ctx.moe_quant(lat, aq, asf, T, KL, stream=s)
+    del lat
+
+    def weights(n, k, gated):
+        w = torch.randint(0, 256, (E * n * k // 2,), generator=g, device="cuda", dtype=torch.uint8)
+        sc = torch.randint(121, 126, (E * n * k // 32,), generator=g, device="cuda",
+                           dtype=torch.uint8)
+        wt, st = torch.empty_like(w), torch.empty_like(sc)
+        ctx.moe_w_tile(w, wt, E, n, k, gated, stream=s)
+        ctx.moe_sf_tile(sc, st, E, n, k, gated, stream=s)
+        return wt, st
+    w13, s13 = weights(2 * INTER, KL, 1)
+    w2, s2 = weights(COLS, INTER, 0)
+    alpha = torch.full((E,), 4.0, device="cuda")
+    beta = torch.full((E,), 25.0, device="cuda")
+    o1 = torch.empty((max_tiles * 128, INTER), dtype=torch.uint8, device="cuda")
+    o1sf = torch.empty((max_tiles * 128, INTER // 32), dtype=torch.uint8, device="cuda")
+    o2 = torch.empty((max_tiles * 128, COLS), dtype=torch.bfloat16, device="cuda")
+    torch.cuda.synchronize()
+    add_flop("MoE fc1 (MX GEMM + SiTU-GLU + MXFP8)", "kern_k3h_moe_gemm_situ_mx",
+             f"{tpad} rows x {KL} -> 2x{INTER}, E={E}", 2 * tpad * KL * 2 * INTER,
+             E * 2 * INTER * (KL // 2 + KL // 32) + tpad * (KL + KL // 32) + tpad * (INTER + INTER // 32),
+             timed(lambda: ctx.moe_gemm_mx(ctx.GEMM_SITU_MX, aq, asf, rmap, w13, s13, num_tiles,
+                                           cta_batch, max_tiles, E, 2 * INTER, KL, o1, o1sf, alpha,
+                                           beta, stream=s)),
+             "e4m3 x e2m1 MFMA; gathers rows through route_map")
+    add_flop("MoE fc2 (MX GEMM, bf16 out)", "kern_k3h_moe_gemm_bf16",
+             f"{tpad} rows x {INTER} -> {COLS}, E={E}", 2 * tpad * INTER * COLS,
+             E * COLS * (INTER // 2 + INTER // 32) + tpad * (INTER + INTER // 32) + tpad * COLS * 2,
+             timed(lambda: ctx.moe_gemm_mx(ctx.GEMM_BF16, o1, o1sf, None, w2, s2, num_tiles,
+                                           cta_batch, max_tiles, E, COLS, INTER, o2, stream=s)),
+             "e4m3 x e2m1 MFMA")
+    del w13, s13, w2, s2, o1, o1sf, o2, aq, asf
+
+
 # Per-op kernels, in launch order, for the counter table (kernel names as the
 # rocprofv3 CSV output prints them).
 OP_KERNELS = {
@@ -369,6 +431,8 @@ OP_KERNELS = {
     "SiTU landing f32 (n 6144)": ["kern_k3_land_situ"],
     "SiTU landing bf16 (l0, n 33792)": ["kern_k3_situ_bf16"],
     "SiTU landing + latent rms (fused)": ["kern_k3_situ_rms_bf16"],
+    "MoE fc1 (MX GEMM + SiTU-GLU + MXFP8)": ["kern_k3h_moe_gemm_situ_mx"],
+    "MoE fc2 (MX GEMM, bf16 out)": ["kern_k3h_moe_gemm_bf16"],
 }
 
 

@@ -298,10 +298,11 @@ K3H_API int k3h_mla_rope_pack(k3h_ctx_t ctx, void* stream, const void* latent,
  * [rows, K] (16-byte aligned rows) with E8M0 a_sf [rows, K/32]; src(r) =
  * a_rows[r] when a_rows (route_map) is given, else r.  Epilogue:
  *   K3H_GEMM_F32      out f32 [tiles*128, N];
- *   K3H_GEMM_BF16     out bf16 [tiles*128, N] (fc2);
+ *   K3H_GEMM_BF16     out bf16 [tiles*128, N] (fc2; 16-byte aligned);
  *   K3H_GEMM_SITU_MX  gated weights: x = bf16(situ(bf16(gate), bf16(up);
- *                     alpha[e], beta[e])) -> out e4m3 [.., N/2], out_sf E8M0
- *                     [.., N/64], quantised as kern_k3_moe_quant (fc1).
+ *                     alpha[e], beta[e])) -> out e4m3 [.., N/2] (16-byte
+ *                     aligned), out_sf E8M0 [.., N/64] (2-byte aligned),
+ *                     quantised as kern_k3_moe_quant (fc1).
  * The grid is (N/256, max_tiles); tiles >= *num_tiles exit.  N % 256 == 0,
  * K % 128 == 0; rows of padding tiles route token 0 and are computed. */
 #define K3H_GEMM_F32 0

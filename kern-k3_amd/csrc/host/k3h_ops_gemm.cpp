@@ -79,12 +79,12 @@ K3H_API int k3h_moe_gemm_mx(k3h_ctx_t ctx, void* stream, int epilogue, const voi
       entry = "kern_k3h_moe_gemm_f32";
       break;
     case K3H_GEMM_BF16:
-      if (!k3h_okp(out, 2)) return K3H_EINVAL;
+      if (!k3h_okp(out, 16)) return K3H_EINVAL;
       args.ptr(out);
       entry = "kern_k3h_moe_gemm_bf16";
       break;
     case K3H_GEMM_SITU_MX:
-      if (!k3h_okp(out, 1) || !k3h_okp(out_sf, 1) || !k3h_okp(alpha, 4) || !k3h_okp(beta, 4))
+      if (!k3h_okp(out, 16) || !k3h_okp(out_sf, 2) || !k3h_okp(alpha, 4) || !k3h_okp(beta, 4))
         return K3H_EINVAL;
       args.ptr(out).ptr(out_sf).ptr(alpha).ptr(beta);
       entry = "kern_k3h_moe_gemm_situ_mx";

@@ -41,12 +41,16 @@
 //
 // Work split: workgroup (x, t) = 256 logical columns x route tile t; 4 waves,
 // wave w owns rows 64 (w / 2) .. + 64 and columns 128 (w % 2) .. + 128 (2 x 4
-// MFMA tiles, 128 accumulator registers); K steps of 128, the next step's
-// operands loaded while this step's 16 MFMAs run.  Consecutive x of a tile land
-// on consecutive XCDs (round-robin dispatch), and with N / 256 a multiple of 8
-// every tile's column block x stays on XCD x % 8, so each XCD's L2 holds one
-// eighth of every expert's weights.
+// MFMA tiles, 128 accumulators).  K steps of 128: the workgroup's A rows, B
+// tiles and scales of a step are brought into LDS by direct-to-LDS loads one
+// step ahead of the MFMAs (two stages; two workgroups per CU).  The epilogues
+// pass the accumulators through LDS so that each lane owns whole output rows
+// (16-byte stores; the fc1 MX blocks quantised in registers).  Consecutive x of
+// a tile land on consecutive XCDs (round-robin dispatch), and with N / 256 a
+// multiple of 8 every tile's column block x stays on XCD x % 8, so each XCD's
+// L2 holds one eighth of every expert's weights.
 #include "../common/k3_dev.h"
+#include "k3_mx.h"
 #include "k3_situ.h"
 
 typedef int k3_v8i __attribute__((ext_vector_type(8)));
@@ -152,6 +156,142 @@ K3_DEV void k3g_mma(k3_v16f (&acc)[2][4], const K3gStep& st, int h) {
   }
 }
 
+#ifndef K3G_LDS
+#define K3G_LDS 1
+#endif
+
+// ---------------------------------------------------------------- LDS pipeline
+// Workgroup-shared operand stages filled by direct-to-LDS loads
+// (global_load_lds_dwordx4: lane l's 16 bytes land at base + 16 l, so every
+// 1 KB block is one MFMA operand in lane order).  A stage (one K step of 128):
+//   A  16 KB: block ((m * 2 + s) * 2 + part), m = 32-row group, s = substep,
+//             part 0/1 = the bytes of k 16 h .. / 32 + 16 h .. of the substep;
+//   B  16 KB: block (T * 2 + s), T = 32-column tile of the workgroup (a copy of
+//             the tiled weights' 1 KB operand);
+//   SA 1 KB:  per wave 256 B: the 4 scale bytes of the step for its 32 rows
+//             (lanes 32..63 repeat lanes 0..31 into the upper 128 B);
+//   SB 1 KB:  the tiled scale pairs of the 8 column tiles (128 B each).
+// Each wave issues 10 loads per stage (4 A blocks of its own 32-row group, 4 B
+// blocks, its 32 rows' A scales from half the wave, one dword per lane of B
+// scales); stages run K3G_STAGES - 1 steps ahead of the MFMAs.
+// Two stages (68 KB) and at most 256 registers per wave let two workgroups share
+// a CU, so one computes while the other waits at its step barrier (measured:
+// 3 stages at one workgroup per CU ran fc1 / fc2 at 1215 / 549 us, 2 stages at
+// two per CU at 832 / 466 us).
+#ifndef K3G_STAGES
+#define K3G_STAGES 2
+#endif
+#ifndef K3G_WAVES_PER_EU
+#define K3G_WAVES_PER_EU 2
+#endif
+#define K3G_SA_OFF 32768
+#define K3G_SB_OFF (32768 + 1024)
+#define K3G_STAGE_BYTES (32768 + 1024 + 1024)
+#define K3G_LOADS_PER_STAGE 10
+
+typedef __attribute__((address_space(3))) void k3g_lds_t;
+
+// The workgroup's LDS: the operand stages of the main loop, then the epilogue's
+// transposition tiles (one object shared by every caller in a kernel).
+K3_DEV uint8_t* k3g_smem() {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[K3G_STAGES * K3G_STAGE_BYTES];
+  return smem;
+}
+
+K3_DEV constexpr int k3g_vmcnt(int n) {  // s_waitcnt vmcnt(n), other counters unconstrained
+  return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8);
+}
+
+K3_DEV void k3g_issue_stage(uint8_t* st, const uint8_t* arow, const uint8_t* sarow,
+                            const uint8_t* wblk, const uint8_t* wsblk, int ks, int KT, int KS,
+                            int w, int lane) {
+  const int h = lane >> 5;
+  const int k0 = ks * K3G_KSTEP;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {  // A blocks of 32-row group w: (s, part) = (b >> 1, b & 1)
+    const int s = b >> 1, part = b & 1;
+    __builtin_amdgcn_global_load_lds(arow + k0 + 64 * s + 32 * part + 16 * h,
+                                     (k3g_lds_t*)(st + ((w * 2 + s) * 2 + part) * 1024), 16, 0, 0);
+  }
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {  // B blocks: tiles 2 w, 2 w + 1, both substeps
+    const int T = 2 * w + (b >> 1), s = b & 1;
+    __builtin_amdgcn_global_load_lds(wblk + ((size_t)T * KT + 2 * ks + s) * 1024 + 16 * lane,
+                                     (k3g_lds_t*)(st + 16384 + (T * 2 + s) * 1024), 16, 0, 0);
+  }
+  // A scales: lanes 0..31 load the dwords of rows 32 w + lane (lanes 32..63 load the
+  // same dwords again into the next 128 bytes, which nobody reads)
+  __builtin_amdgcn_global_load_lds(sarow + ks * 4, (k3g_lds_t*)(st + K3G_SA_OFF + w * 256), 4,
+                                   0, 0);
+  // B scales: dword lane of tiles 2 w + lane / 32
+  __builtin_amdgcn_global_load_lds(
+      wsblk + ((size_t)(2 * w + (lane >> 5)) * KS + ks) * 128 + 4 * (lane & 31),
+      (k3g_lds_t*)(st + K3G_SB_OFF + w * 256), 4, 0, 0);
+}
+
+K3_DEV void k3g_lds_loop(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
+                         const uint8_t* __restrict__ a_sf, const int* __restrict__ a_rows,
+                         const uint8_t* __restrict__ wt, const uint16_t* __restrict__ wsf, int tile,
+                         int e, int N, int K, int w, int lane, int wm, int wn) {
+  uint8_t* lds = k3g_smem();
+  const int h = lane >> 5, j = lane & 31;
+  const int KG = K / 32, KT = K / 64, KS = K / K3G_KSTEP, NT = N / 32;
+  // this wave's loads: rows 32 w + j of the tile (A operand blocks and scales)
+  const int r = tile * K3G_TILE_M + 32 * w + j;
+  int src = a_rows ? a_rows[r] : r;
+  src = src < 0 ? 0 : src;
+  const uint8_t* arow = a + (size_t)src * K;
+  const uint8_t* sarow = a_sf + (size_t)src * KG;
+  const size_t T0 = (size_t)e * NT + blockIdx.x * (K3G_TILE_N / 32);
+  const uint8_t* wblk = wt + T0 * KT * 1024;
+  const uint8_t* wsblk = (const uint8_t*)wsf + T0 * KS * 128;
+
+#pragma unroll
+  for (int p = 0; p < K3G_STAGES - 1; ++p)
+    if (p < KS) k3g_issue_stage(lds + p * K3G_STAGE_BYTES, arow, sarow, wblk, wsblk, p, KT, KS, w, lane);
+
+  for (int ks = 0; ks < KS; ++ks) {
+    // this wave's loads of step ks are done once at most the later issued stages remain
+    if (ks + 1 < KS) __builtin_amdgcn_s_waitcnt(k3g_vmcnt(K3G_LOADS_PER_STAGE * (K3G_STAGES - 2)));
+    else __builtin_amdgcn_s_waitcnt(k3g_vmcnt(0));
+    __builtin_amdgcn_s_barrier();  // every wave's loads of step ks landed; stage ks - 1 is free
+    if (ks + K3G_STAGES - 1 < KS)
+      k3g_issue_stage(lds + ((ks + K3G_STAGES - 1) % K3G_STAGES) * K3G_STAGE_BYTES, arow, sarow,
+                      wblk, wsblk, ks + K3G_STAGES - 1, KT, KS, w, lane);
+    const uint8_t* st = lds + (ks % K3G_STAGES) * K3G_STAGE_BYTES;
+    uint32_t sa[2], sb[4];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+      sa[mt] = *(const uint32_t*)(st + K3G_SA_OFF + (2 * wm + mt) * 256 + 4 * j);
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+      sb[nt] = *(const uint16_t*)(st + K3G_SB_OFF + (4 * wn + nt) * 128 + 2 * lane);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      k3_v8i av[2];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const int m = 2 * wm + mt;
+        const k3_u4 lo = *(const k3_u4*)(st + ((m * 2 + s) * 2 + 0) * 1024 + 16 * lane);
+        const k3_u4 hi = *(const k3_u4*)(st + ((m * 2 + s) * 2 + 1) * 1024 + 16 * lane);
+        av[mt] = (k3_v8i){(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
+                          (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+      }
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const int T = 4 * wn + nt;
+        const k3_u4 bv = *(const k3_u4*)(st + 16384 + (T * 2 + s) * 1024 + 16 * lane);
+        const k3_v8i b = {(int)bv[0], (int)bv[1], (int)bv[2], (int)bv[3], 0, 0, 0, 0};
+        const int sbv = (int)(sb[nt] >> (8 * s));
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+              av[mt], b, acc[mt][nt], 0, 4, 0, (int)(sa[mt] >> (16 * s + 8 * h)), 0, sbv);
+      }
+    }
+  }
+}
+
 // Accumulates the wave's 64 x 128 block; returns false when the tile is past
 // the routing tables' live count or its expert is out of range (the whole
 // workgroup exits).
@@ -196,6 +336,9 @@ K3_DEV bool k3g_block(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
 #pragma unroll
       for (int q = 0; q < 16; ++q) acc[mt][nt][q] = 0.0f;
 
+#if K3G_LDS
+  k3g_lds_loop(acc, a, a_sf, a_rows, wt, wsf, tile, e, N, K, w, lane, wm, wn);
+#else
   K3gStep cur, nxt;
   k3g_load(cur, ap, sp, wp, wsp, 0, h);
   for (int ks = 0; ks < KS; ++ks) {
@@ -203,6 +346,7 @@ K3_DEV bool k3g_block(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
     k3g_mma(acc, cur, h);
     cur = nxt;
   }
+#endif
   return true;
 }
 
@@ -217,7 +361,7 @@ K3_DEV int k3g_out_row(int wm, int mt, int q, int h) {
       const uint16_t *__restrict__ wsf, const int *__restrict__ num_tiles,                  \
       const int *__restrict__ cta_batch, int E, int N, int K
 
-extern "C" __global__ void __launch_bounds__(256) kern_k3h_moe_gemm_f32(K3G_PARAMS,
+extern "C" __global__ void __launch_bounds__(256, K3G_WAVES_PER_EU) kern_k3h_moe_gemm_f32(K3G_PARAMS,
                                                                         float* __restrict__ out) {
   k3_v16f acc[2][4];
   int tile, e, lane, wm, wn;
@@ -237,45 +381,47 @@ extern "C" __global__ void __launch_bounds__(256) kern_k3h_moe_gemm_f32(K3G_PARA
     }
 }
 
-extern "C" __global__ void __launch_bounds__(256) kern_k3h_moe_gemm_bf16(K3G_PARAMS,
+// Epilogue transposition: each wave writes its 64 x 128 block (bf16) to its own
+// LDS tile, row stride K3G_EP_ROW bytes (padded so that the column writes of the
+// two half-waves and the 16-byte row reads hit different banks); lane l then
+// owns row l and stores it with 16-byte writes.
+#define K3G_EP_ROW 272
+#define K3G_EP_TILE (64 * K3G_EP_ROW)
+
+extern "C" __global__ void __launch_bounds__(256, K3G_WAVES_PER_EU) kern_k3h_moe_gemm_bf16(K3G_PARAMS,
                                                                          uint16_t* __restrict__ out) {
   k3_v16f acc[2][4];
   int tile, e, lane, wm, wn;
   if (!k3g_block(acc, a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch, E, N, K, tile, e, lane, wm, wn))
     return;
   const int h = lane >> 5, j = lane & 31;
+  __syncthreads();  // every wave is done with the operand stages
+  uint8_t* wl = k3g_smem() + (threadIdx.x >> 6) * K3G_EP_TILE;
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      const int col = blockIdx.x * K3G_TILE_N + 128 * wn + 32 * nt + j;
+    for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
-        const size_t row = (size_t)tile * K3G_TILE_M + k3g_out_row(wm, mt, q, h);
-        out[row * N + col] = (uint16_t)k3_pack_bf2(acc[mt][nt][q], 0.0f);
+        const int r = 32 * mt + 8 * (q >> 2) + 4 * h + (q & 3);
+        *(uint16_t*)(wl + r * K3G_EP_ROW + 2 * (32 * nt + j)) =
+            (uint16_t)k3_pack_bf2(acc[mt][nt][q], 0.0f);
       }
-    }
+  __syncthreads();
+  uint16_t* orow = out + ((size_t)tile * K3G_TILE_M + 64 * wm + lane) * N + blockIdx.x * K3G_TILE_N +
+                   128 * wn;
+#pragma unroll
+  for (int c = 0; c < 16; ++c) k3_st16(orow + 8 * c, *(const k3_u4*)(wl + lane * K3G_EP_ROW + 16 * c));
 }
 
-// One bf16 value scaled by 2^-e to e4m3 (byte), as k3_vec_to_e4m3 does per element.
-K3_DEV uint32_t k3g_to_e4m3(uint32_t xb16, int e) {
-  const float f = __builtin_ldexpf(k3_bf((uint16_t)xb16), -e);
-  uint32_t q = k3_pack_e4m3x2(f, 0.0f) & 0xffu;
-  if (e == 127 && __builtin_isinf(f)) q = 0x7eu | (f < 0.0f ? 0x80u : 0u);
-  return q;
-}
+// fc1 epilogue: the activation of the wave's 64 rows x 64 activation columns
+// goes through LDS (row stride K3G_ACT_ROW bytes, padded as above); lane l then
+// holds row l's two 32-column MX blocks and quantises them in registers as
+// kern_k3_moe_quant does (block amax of the bf16 patterns, E8M0 exponent,
+// e4m3 of x * 2^-e), with 16-byte payload stores and one 2-byte scale store.
+#define K3G_ACT_ROW 144
 
-// Largest value over the 32 lanes of this half-wave (ds_swizzle xor butterfly).
-K3_DEV uint32_t k3g_max32_u32(uint32_t v) {
-  uint32_t o = k3_swz_xor_u32<16>(v); v = v > o ? v : o;
-  o = k3_swz_xor_u32<8>(v); v = v > o ? v : o;
-  o = k3_swz_xor_u32<4>(v); v = v > o ? v : o;
-  o = k3_swz_xor_u32<2>(v); v = v > o ? v : o;
-  o = k3_swz_xor_u32<1>(v); v = v > o ? v : o;
-  return v;
-}
-
-extern "C" __global__ void __launch_bounds__(256) kern_k3h_moe_gemm_situ_mx(
+extern "C" __global__ void __launch_bounds__(256, K3G_WAVES_PER_EU) kern_k3h_moe_gemm_situ_mx(
     K3G_PARAMS, uint8_t* __restrict__ out_q, uint8_t* __restrict__ out_sf,
     const float* __restrict__ alpha, const float* __restrict__ beta) {
   k3_v16f acc[2][4];
@@ -286,22 +432,42 @@ extern "C" __global__ void __launch_bounds__(256) kern_k3h_moe_gemm_situ_mx(
   const float al = alpha[e], be = beta[e];
   const float ial = 1.0f / al, ibe = 1.0f / be;
   const int NA = N / 2;  // activation columns
+  __syncthreads();       // every wave is done with the operand stages
+  uint8_t* wl = k3g_smem() + (threadIdx.x >> 6) * (64 * K3G_ACT_ROW);
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      // logical tiles 2 t (up) and 2 t + 1 (gate): activation block t
-      const int t = blockIdx.x * (K3G_TILE_N / 64) + 2 * wn + p;
+    for (int p = 0; p < 2; ++p)
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
+        // logical tiles 4 wn + 2 p (up) and 4 wn + 2 p + 1 (gate): activation columns 32 p + j
         const float u = k3_land(acc[mt][2 * p][q]);
         const float g = k3_land(acc[mt][2 * p + 1][q]);
-        const uint32_t xb = k3_pack_bf2(k3_situ_gate_a(g, al, ial) * k3_situ_up_b(u, be, ibe), 0.0f);
-        const int ex = k3_e8m0_exp(k3g_max32_u32(k3_absbits_nonan(xb & 0xffffu)));
-        const uint32_t qb = k3g_to_e4m3(xb, ex);
-        const size_t row = (size_t)tile * K3G_TILE_M + k3g_out_row(wm, mt, q, h);
-        out_q[row * NA + 32 * t + j] = (uint8_t)qb;
-        if (j == 0) out_sf[row * (NA / 32) + t] = (uint8_t)(ex + 127);
+        const int r = 32 * mt + 8 * (q >> 2) + 4 * h + (q & 3);
+        *(uint16_t*)(wl + r * K3G_ACT_ROW + 2 * (32 * p + j)) =
+            (uint16_t)k3_pack_bf2(k3_situ_gate_a(g, al, ial) * k3_situ_up_b(u, be, ibe), 0.0f);
       }
+  __syncthreads();
+  const size_t row = (size_t)tile * K3G_TILE_M + 64 * wm + lane;
+  const int col0 = 64 * (2 * blockIdx.x + wn);  // this wave's first activation column
+  uint32_t sfp = 0;
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    k3_u4 v[4];
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = *(const k3_u4*)(wl + lane * K3G_ACT_ROW + 64 * c + 16 * i);
+      const uint32_t mi = k3_vec_absmax_bits(v[i]);
+      m = m > mi ? m : mi;
     }
+    const int ex = k3_e8m0_exp(m);
+    const k3_u2 q0 = k3_vec_to_e4m3(v[0], ex), q1 = k3_vec_to_e4m3(v[1], ex);
+    const k3_u2 q2 = k3_vec_to_e4m3(v[2], ex), q3 = k3_vec_to_e4m3(v[3], ex);
+    uint8_t* o = out_q + row * NA + col0 + 32 * c;
+    k3_st16(o, (k3_u4){q0[0], q0[1], q1[0], q1[1]});
+    k3_st16(o + 16, (k3_u4){q2[0], q2[1], q3[0], q3[1]});
+    sfp |= (uint32_t)(ex + 127) << (8 * c);
+  }
+  *(uint16_t*)(out_sf + row * (NA / 32) + col0 / 32) = (uint16_t)sfp;
 }

@@ -606,10 +606,10 @@ class Ctx:
         if epilogue == self.GEMM_F32:
             _dev(out, "out", F32, rows * N, align=4)
         elif epilogue == self.GEMM_BF16:
-            _dev(out, "out", BF16, rows * N, align=2)
+            _dev(out, "out", BF16, rows * N, align=16)
         else:
-            _dev(out, "out", U8, rows * N // 2, align=1)
-            _dev(out_sf, "out_sf", U8, rows * N // 64, align=1)
+            _dev(out, "out", U8, rows * N // 2, align=16)
+            _dev(out_sf, "out_sf", U8, rows * N // 64, align=2)
             _dev(alpha, "alpha", F32, E, align=4)
             _dev(beta, "beta", F32, E, align=4)
         _check(self.L.k3h_moe_gemm_mx(self.h, _stream(stream), epilogue, _ptr(a), _ptr(a_sf),
