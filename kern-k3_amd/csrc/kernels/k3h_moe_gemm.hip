@@ -255,9 +255,7 @@ K3_DEV void k3g_lds_loop(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
     if (ks + 1 < KS) __builtin_amdgcn_s_waitcnt(k3g_vmcnt(K3G_LOADS_PER_STAGE * (K3G_STAGES - 2)));
     else __builtin_amdgcn_s_waitcnt(k3g_vmcnt(0));
     __builtin_amdgcn_s_barrier();  // every wave's loads of step ks landed; stage ks - 1 is free
-    if (ks + K3G_STAGES - 1 < KS)
-      k3g_issue_stage(lds + ((ks + K3G_STAGES - 1) % K3G_STAGES) * K3G_STAGE_BYTES, arow, sarow,
-                      wblk, wsblk, ks + K3G_STAGES - 1, KT, KS, w, lane);
+                                   // (its last reads were before this barrier)
     const uint8_t* st = lds + (ks % K3G_STAGES) * K3G_STAGE_BYTES;
     uint32_t sa[2], sb[4];
 #pragma unroll
@@ -288,6 +286,11 @@ K3_DEV void k3g_lds_loop(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
           acc[mt][nt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
               av[mt], b, acc[mt][nt], 0, 4, 0, (int)(sa[mt] >> (16 * s + 8 * h)), 0, sbv);
       }
+      // the next stage's loads go out behind the first substep's MFMAs, so that the
+      // matrix cores start right after the barrier
+      if (s == 0 && ks + K3G_STAGES - 1 < KS)
+        k3g_issue_stage(lds + ((ks + K3G_STAGES - 1) % K3G_STAGES) * K3G_STAGE_BYTES, arow, sarow,
+                        wblk, wsblk, ks + K3G_STAGES - 1, KT, KS, w, lane);
     }
   }
 }
