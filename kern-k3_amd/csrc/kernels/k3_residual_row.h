@@ -129,6 +129,13 @@ K3_DEV void k3_attnres_mix(const uint16_t* __restrict__ blk_row, k3_u4* pv,
   constexpr int PF = 1;
   constexpr bool RES = NBC >= 1 && NBC <= 2;
   k3_u4 xr[RES ? NBC : 1][K3_KVPT];
+  // HOLD: with a compile-time nb >= 3 (and no statistics hand-off) the first
+  // HOLD vector steps of every candidate stay in registers from pass 1 to pass 2;
+  // pass 2 re-reads only the later steps, which pass 1 read last.  Measured at
+  // B = 4096 (the nb entries): nb 5 165 -> 157 us, nb 8 207 -> 201 us, nb 3, 4, 6
+  // within 1-2%, nb 7 none (the registers would push it to one wave per SIMD).
+  constexpr int HOLD = (RES || SIN) ? 0 : (NBC >= 3 && NBC <= 6) ? 2 : NBC == 8 ? 1 : 0;
+  k3_u4 xh[HOLD > 0 ? HOLD : 1][K3_NB_MAX];
   if constexpr (RES) {
 #pragma unroll
     for (int c = 0; c < NBC; ++c)
@@ -195,6 +202,9 @@ K3_DEV void k3_attnres_mix(const uint16_t* __restrict__ blk_row, k3_u4* pv,
       k3_u4 x;
       if constexpr (RES) x = xr[c][v];
       else x = xb[slot][c];
+      if constexpr (HOLD > 0) {
+        if (v < HOLD) xh[v < HOLD ? v : 0][c] = x;
+      }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const float lo = k3_bf_lo(x[j]), hi = k3_bf_hi(x[j]);
@@ -287,7 +297,7 @@ K3_DEV void k3_attnres_mix(const uint16_t* __restrict__ blk_row, k3_u4* pv,
   for (int w = 0; w < K3_KVPT; ++w) {
     const int v = K3_KVPT - 1 - w;
     const int slot = w % (PF + 1);
-    if (w + PF < K3_KVPT) load2(v - PF, (w + PF) % (PF + 1), dep2);
+    if (w + PF < K3_KVPT && v - PF >= HOLD) load2(v - PF, (w + PF) % (PF + 1), dep2);
     const k3_u4* xv = xb[slot];
     float acc[8];
 #pragma unroll
@@ -300,6 +310,7 @@ K3_DEV void k3_attnres_mix(const uint16_t* __restrict__ blk_row, k3_u4* pv,
       if (c >= nb) break;
       k3_u4 x;
       if constexpr (RES) x = xr[c][v];
+      else if (HOLD > 0 && v < HOLD) x = xh[v < HOLD ? v : 0][c];
       else x = xv[c];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
