@@ -88,6 +88,7 @@ K3_DEV float k3_row_rscale(float tot, float eps) {
 // stats rows are [K3_NB_MAX][2] floats.
 #define K3_MIX_STATS_OUT 1
 #define K3_MIX_STATS_IN 2
+#define K3_MIX_NO_HOLD 4  /* keep no vector steps across the passes (register budget) */
 
 // Zero that the compiler cannot see through, computed after `dep`.  Added to
 // the addresses of a vector step's loads, it keeps them from being issued
@@ -134,7 +135,8 @@ K3_DEV void k3_attnres_mix(const uint16_t* __restrict__ blk_row, k3_u4* pv,
   // pass 2 re-reads only the later steps, which pass 1 read last.  Measured at
   // B = 4096 (the nb entries): nb 5 165 -> 157 us, nb 8 207 -> 201 us, nb 3, 4, 6
   // within 1-2%, nb 7 none (the registers would push it to one wave per SIMD).
-  constexpr int HOLD = (RES || SIN) ? 0 : (NBC >= 3 && NBC <= 6) ? 2 : NBC == 8 ? 1 : 0;
+  constexpr int HOLD = (RES || SIN || (MODE & K3_MIX_NO_HOLD)) ? 0
+                       : (NBC >= 3 && NBC <= 6) ? 2 : NBC == 8 ? 1 : 0;
   k3_u4 xh[HOLD > 0 ? HOLD : 1][K3_NB_MAX];
   if constexpr (RES) {
 #pragma unroll
@@ -359,6 +361,27 @@ K3_DEV void k3_attnres_rms_row_to(const uint16_t* __restrict__ blk_row, k3_u4* p
                                   const float* __restrict__ sw_mlp = nullptr,
                                   float* __restrict__ stats_out = nullptr,
                                   const float* __restrict__ stats_in = nullptr, int nb_stats = 0) {
+#ifndef K3_NB_SWITCH
+#define K3_NB_SWITCH 1
+#endif
+  if constexpr (NBC < 0 && K3_NB_SWITCH) {
+    // run-time nb: branch once (uniformly) into the compile-time instantiation,
+    // which drops the unused candidate registers and guards and keeps one or two
+    // candidates resident (no held vector steps: every instantiation shares the
+    // kernel's register budget)
+#define K3_NB_CASE(K)                                                                         \
+  case K:                                                                                     \
+    k3_attnres_rms_row_to<K, MODE | K3_MIX_NO_HOLD>(blk_row, pv, sw, gamma, dst, K, eps, t,   \
+                                                    sw_mlp, stats_out, stats_in, nb_stats);   \
+    return;
+    switch (nb) {
+      K3_NB_CASE(0) K3_NB_CASE(1) K3_NB_CASE(2) K3_NB_CASE(3) K3_NB_CASE(4)
+      K3_NB_CASE(5) K3_NB_CASE(6) K3_NB_CASE(7) K3_NB_CASE(8)
+      default:
+        break;
+    }
+#undef K3_NB_CASE
+  }
   __shared__ float s_red2[K3_NHW];
   k3_attnres_mix<NBC, MODE>(blk_row, pv, sw, nb, eps, t, sw_mlp, stats_out, stats_in, nb_stats);
   const float tot = k3_block_sum128(k3_row_sumsq(pv), s_red2, t);
