@@ -162,18 +162,20 @@ K3_DEV void k3g_mma(k3_v16f (&acc)[2][4], const K3gStep& st, int h) {
 
 // ---------------------------------------------------------------- LDS pipeline
 // Workgroup-shared operand stages filled by direct-to-LDS loads
-// (global_load_lds_dwordx4: lane l's 16 bytes land at base + 16 l, so every
-// 1 KB block is one MFMA operand in lane order).  A stage (one K step of 128):
-//   A  16 KB: block ((m * 2 + s) * 2 + part), m = 32-row group, s = substep,
-//             part 0/1 = the bytes of k 16 h .. / 32 + 16 h .. of the substep;
+// (global_load_lds_dwordx4: lane l's 16 bytes land at base + 16 l).  A stage
+// (one K step of 128):
+//   A  16 KB: the 128 rows' 128-byte slices, swizzled (k3g_aslot); each load
+//             instruction moves 8 whole row slices (measured: loading the same
+//             bytes as 32 rows x 32 bytes per instruction, in MFMA operand order,
+//             cost a third of the kernel's time);
 //   B  16 KB: block (T * 2 + s), T = 32-column tile of the workgroup (a copy of
 //             the tiled weights' 1 KB operand);
 //   SA 1 KB:  per wave 256 B: the 4 scale bytes of the step for its 32 rows
 //             (lanes 32..63 repeat lanes 0..31 into the upper 128 B);
 //   SB 1 KB:  the tiled scale pairs of the 8 column tiles (128 B each).
-// Each wave issues 10 loads per stage (4 A blocks of its own 32-row group, 4 B
-// blocks, its 32 rows' A scales from half the wave, one dword per lane of B
-// scales); stages run K3G_STAGES - 1 steps ahead of the MFMAs.
+// Each wave issues 10 loads per stage (its 32 rows' A slices in 4, 4 B blocks,
+// its 32 rows' A scales from half the wave, one dword per lane of B scales);
+// stages run K3G_STAGES - 1 steps ahead of the MFMAs.
 // Two stages (68 KB) and at most 256 registers per wave let two workgroups share
 // a CU, so one computes while the other waits at its step barrier (measured:
 // 3 stages at one workgroup per CU ran fc1 / fc2 at 1215 / 549 us, 2 stages at
@@ -202,17 +204,22 @@ K3_DEV constexpr int k3g_vmcnt(int n) {  // s_waitcnt vmcnt(n), other counters u
   return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8);
 }
 
-K3_DEV void k3g_issue_stage(uint8_t* st, const uint8_t* arow, const uint8_t* sarow,
+// A rows in LDS: row r of the tile's step slice (128 bytes = 8 chunks of 16) at
+// slots 8 r + (c ^ (r & 7)), c = chunk.  One load instruction moves 8 whole
+// 128-byte row slices (lane l: row 8 q + l / 8, chunk (l % 8) ^ (l / 8)), and the
+// MFMA operand reads (lanes of 8 consecutive rows, one chunk each) hit 8
+// different bank groups.
+K3_DEV int k3g_aslot(int r, int c) { return 8 * r + (c ^ (r & 7)); }
+
+K3_DEV void k3g_issue_stage(uint8_t* st, const uint8_t* const* arow, const uint8_t* sarow,
                             const uint8_t* wblk, const uint8_t* wsblk, int ks, int KT, int KS,
                             int w, int lane) {
-  const int h = lane >> 5;
   const int k0 = ks * K3G_KSTEP;
+  const int c = (lane & 7) ^ (lane >> 3);  // the chunk this lane moves (row 8 q + lane / 8)
 #pragma unroll
-  for (int b = 0; b < 4; ++b) {  // A blocks of 32-row group w: (s, part) = (b >> 1, b & 1)
-    const int s = b >> 1, part = b & 1;
-    __builtin_amdgcn_global_load_lds(arow + k0 + 64 * s + 32 * part + 16 * h,
-                                     (k3g_lds_t*)(st + ((w * 2 + s) * 2 + part) * 1024), 16, 0, 0);
-  }
+  for (int b = 0; b < 4; ++b)  // rows 32 w + 8 b .. + 8 of the tile
+    __builtin_amdgcn_global_load_lds(arow[b] + k0 + 16 * c,
+                                     (k3g_lds_t*)(st + (4 * w + b) * 1024), 16, 0, 0);
 #pragma unroll
   for (int b = 0; b < 4; ++b) {  // B blocks: tiles 2 w, 2 w + 1, both substeps
     const int T = 2 * w + (b >> 1), s = b & 1;
@@ -236,12 +243,19 @@ K3_DEV void k3g_lds_loop(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
   uint8_t* lds = k3g_smem();
   const int h = lane >> 5, j = lane & 31;
   const int KG = K / 32, KT = K / 64, KS = K / K3G_KSTEP, NT = N / 32;
-  // this wave's loads: rows 32 w + j of the tile (A operand blocks and scales)
-  const int r = tile * K3G_TILE_M + 32 * w + j;
-  int src = a_rows ? a_rows[r] : r;
-  src = src < 0 ? 0 : src;
-  const uint8_t* arow = a + (size_t)src * K;
-  const uint8_t* sarow = a_sf + (size_t)src * KG;
+  // this wave's loads: A rows 32 w + 8 b + lane / 8 (b < 4), scale rows 32 w + j
+  const uint8_t* arow[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int r = tile * K3G_TILE_M + 32 * w + 8 * b + (lane >> 3);
+    int src = a_rows ? a_rows[r] : r;
+    src = src < 0 ? 0 : src;
+    arow[b] = a + (size_t)src * K;
+  }
+  const int rs = tile * K3G_TILE_M + 32 * w + j;
+  int ssrc = a_rows ? a_rows[rs] : rs;
+  ssrc = ssrc < 0 ? 0 : ssrc;
+  const uint8_t* sarow = a_sf + (size_t)ssrc * KG;
   const size_t T0 = (size_t)e * NT + blockIdx.x * (K3G_TILE_N / 32);
   const uint8_t* wblk = wt + T0 * KT * 1024;
   const uint8_t* wsblk = (const uint8_t*)wsf + T0 * KS * 128;
@@ -269,9 +283,9 @@ K3_DEV void k3g_lds_loop(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
       k3_v8i av[2];
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
-        const int m = 2 * wm + mt;
-        const k3_u4 lo = *(const k3_u4*)(st + ((m * 2 + s) * 2 + 0) * 1024 + 16 * lane);
-        const k3_u4 hi = *(const k3_u4*)(st + ((m * 2 + s) * 2 + 1) * 1024 + 16 * lane);
+        const int r = 32 * (2 * wm + mt) + j;
+        const k3_u4 lo = *(const k3_u4*)(st + 16 * k3g_aslot(r, 4 * s + h));
+        const k3_u4 hi = *(const k3_u4*)(st + 16 * k3g_aslot(r, 4 * s + 2 + h));
         av[mt] = (k3_v8i){(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
                           (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
       }
