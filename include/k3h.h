@@ -292,7 +292,7 @@ K3H_API int k3h_mla_rope_pack(k3h_ctx_t ctx, void* stream, const void* latent,
  * [up; gate] halves (n/2 each) and the tiles alternate up / gate.  n % 32 == 0
  * (n % 64 gated), k % 64 == 0.
  * k3h_moe_sf_tile: E8M0 scales src [experts, n, k/32] -> tiled dst (same size,
- * 2-byte aligned).  k % 128 == 0.
+ * 8-byte aligned).  n % 128 == 0, k % 128 == 0.
  * k3h_moe_gemm_mx: C[r, :] = a(src(r), :) . w_e^T over the route tiles t <
  * *num_tiles (rows [128 t, 128 t + 128), expert e = cta_batch[t]); a e4m3
  * [rows, K] (16-byte aligned rows) with E8M0 a_sf [rows, K/32]; src(r) =
@@ -304,7 +304,8 @@ K3H_API int k3h_mla_rope_pack(k3h_ctx_t ctx, void* stream, const void* latent,
  *                     aligned), out_sf E8M0 [.., N/64] (2-byte aligned),
  *                     quantised as kern_k3_moe_quant (fc1).
  * The grid is (N/256, max_tiles); tiles >= *num_tiles exit.  N % 256 == 0,
- * K % 128 == 0; rows of padding tiles route token 0 and are computed. */
+ * K % 128 == 0, K <= 7168; rows of padding tiles route token 0 and are
+ * computed.  a_rows values (when given) must index rows of a / a_sf. */
 #define K3H_GEMM_F32 0
 #define K3H_GEMM_BF16 1
 #define K3H_GEMM_SITU_MX 2

@@ -16,8 +16,13 @@ namespace {
 constexpr uint32_t kBlock = 256;
 constexpr int kTileN = 256, kStepK = 128;
 
+// The kernels keep the tile's A scales (K / 32 bytes per row) in LDS: entries
+// without a suffix take K <= 3584, the "_w" entries K <= 7168.
+constexpr int kMaxK = 7168, kMaxKNarrow = 3584;
+
 bool gemm_shape_ok(int E, int N, int K, int max_tiles) {
-  return E > 0 && N > 0 && K > 0 && max_tiles >= 0 && N % kTileN == 0 && K % kStepK == 0;
+  return E > 0 && N > 0 && K > 0 && max_tiles >= 0 && N % kTileN == 0 && K % kStepK == 0 &&
+         K <= kMaxK;
 }
 
 K3hArgs gemm_args(const void* a, const void* a_sf, const int* a_rows, const void* wt,
@@ -31,7 +36,7 @@ K3hArgs gemm_args(const void* a, const void* a_sf, const int* a_rows, const void
 bool gemm_ptrs_ok(const void* a, const void* a_sf, const int* a_rows, const void* wt,
                   const void* wsf, const int* num_tiles, const int* cta_batch) {
   return k3h_okp(a, 16) && k3h_okp(a_sf, 4) && (a_rows == nullptr || k3h_aligned(a_rows, 4)) &&
-         k3h_okp(wt, 16) && k3h_okp(wsf, 2) && k3h_okp(num_tiles, 4) && k3h_okp(cta_batch, 4);
+         k3h_okp(wt, 16) && k3h_okp(wsf, 8) && k3h_okp(num_tiles, 4) && k3h_okp(cta_batch, 4);
 }
 }  // namespace
 
@@ -52,10 +57,9 @@ K3H_API int k3h_moe_w_tile(k3h_ctx_t ctx, void* stream, const void* src, void* d
 
 K3H_API int k3h_moe_sf_tile(k3h_ctx_t ctx, void* stream, const void* src, void* dst, int experts,
                             int n, int k, int gated) {
-  if (!ctx || experts < 0 || n <= 0 || k <= 0 || n % 32 || k % 128 || (gated && n % 64))
-    return K3H_EINVAL;
-  if (!k3h_okp(src, 1) || !k3h_okp(dst, 2)) return K3H_EINVAL;
-  const int64_t total = (int64_t)experts * (n / 32) * (k / 128) * 64;
+  if (!ctx || experts < 0 || n <= 0 || k <= 0 || n % 128 || k % 128) return K3H_EINVAL;
+  if (!k3h_okp(src, 1) || !k3h_okp(dst, 8)) return K3H_EINVAL;
+  const int64_t total = (int64_t)experts * (n / 128) * (k / 128) * 64 * 4;
   if (total == 0) return K3H_OK;
   K3hArgs a;
   a.ptr(src).ptr(dst).i32(experts).i32(n).i32(k).i32(gated ? 1 : 0);
@@ -71,23 +75,24 @@ K3H_API int k3h_moe_gemm_mx(k3h_ctx_t ctx, void* stream, int epilogue, const voi
   if (!ctx || !gemm_shape_ok(E, N, K, max_tiles)) return K3H_EINVAL;
   if (!gemm_ptrs_ok(a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch)) return K3H_EINVAL;
   K3hArgs args = gemm_args(a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch, E, N, K);
+  const bool wide = K > kMaxKNarrow;
   const char* entry = nullptr;
   switch (epilogue) {
     case K3H_GEMM_F32:
       if (!k3h_okp(out, 4)) return K3H_EINVAL;
       args.ptr(out);
-      entry = "kern_k3h_moe_gemm_f32";
+      entry = wide ? "kern_k3h_moe_gemm_f32_w" : "kern_k3h_moe_gemm_f32";
       break;
     case K3H_GEMM_BF16:
       if (!k3h_okp(out, 16)) return K3H_EINVAL;
       args.ptr(out);
-      entry = "kern_k3h_moe_gemm_bf16";
+      entry = wide ? "kern_k3h_moe_gemm_bf16_w" : "kern_k3h_moe_gemm_bf16";
       break;
     case K3H_GEMM_SITU_MX:
       if (!k3h_okp(out, 16) || !k3h_okp(out_sf, 2) || !k3h_okp(alpha, 4) || !k3h_okp(beta, 4))
         return K3H_EINVAL;
       args.ptr(out).ptr(out_sf).ptr(alpha).ptr(beta);
-      entry = "kern_k3h_moe_gemm_situ_mx";
+      entry = wide ? "kern_k3h_moe_gemm_situ_mx_w" : "kern_k3h_moe_gemm_situ_mx";
       break;
     default:
       return K3H_EINVAL;

@@ -27,7 +27,10 @@
 //   wt  [E][N / 32][K / 64][64][16 B]: lane l = (j = l % 32, h = l / 32) of the
 //       32-column tile T holds row R(T, j), k in [64 kt + 32 h, + 32) -- exactly
 //       the B operand of one MFMA, so each operand is one 1 KB coalesced load;
-//   wsf [E][N / 32][K / 128][64][2 B]: byte s = scale block 4 ks + 2 s + h of R(T, j).
+//   wsf [E][N / 128][K / 128][64][4][2 B]: for the 4 consecutive column tiles
+//       T = 4 G + u of group G, byte s of entry (ks, lane l, u) = scale block
+//       4 ks + 2 s + h of R(T, j) -- a wave's 4 tiles' scales of one K step are
+//       one 8-byte load per lane.
 //   R(T, j) = 32 T + j, or for the gated fc1 weights (tile order up, gate, up,
 //   gate, ...) R(2 t, j) = 32 t + j (up) and R(2 t + 1, j) = N / 2 + 32 t + j (gate),
 //   so a wave holds an up tile and its gate tile in the same accumulator lanes.
@@ -87,78 +90,27 @@ extern "C" __global__ void __launch_bounds__(256) kern_k3h_moe_w_tile(
   }
 }
 
-// One thread per (e, T, ks, l): two scale bytes.
+// One thread per (e, G, ks, l, u): two scale bytes (u fastest).
 extern "C" __global__ void __launch_bounds__(256) kern_k3h_moe_sf_tile(
     const uint8_t* __restrict__ src, uint16_t* __restrict__ dst, int experts, int n, int k,
     int gated) {
-  const long long NT = n / 32, KS = k / 128, KG = k / 32;
-  const long long total = (long long)experts * NT * KS * 64;
+  const long long NG = n / 128, KS = k / 128, KG = k / 32;
+  const long long total = (long long)experts * NG * KS * 64 * 4;
   for (long long id = (long long)blockIdx.x * blockDim.x + threadIdx.x; id < total;
        id += (long long)gridDim.x * blockDim.x) {
-    const int l = (int)(id & 63);
-    const long long q = id >> 6;
+    const int u = (int)(id & 3);
+    long long q = id >> 2;
+    const int l = (int)(q & 63);
+    q >>= 6;
     const int ks = (int)(q % KS);
-    const long long et = q / KS;
-    const int T = (int)(et % NT);
-    const long long e = et / NT;
-    const int r = k3g_row(T, l & 31, n, gated);
+    q /= KS;
+    const int G = (int)(q % NG);
+    const long long e = q / NG;
+    const int r = k3g_row(4 * G + u, l & 31, n, gated);
     const uint8_t* s = src + (e * n + r) * KG + 4 * ks + (l >> 5);
     dst[id] = (uint16_t)(s[0] | (s[2] << 8));
   }
 }
-
-// ---------------------------------------------------------------- main loop
-struct K3gStep {
-  k3_u4 alo[2][2], ahi[2][2];  // [m tile][substep]
-  uint32_t sa[2];              // A scale bytes of blocks 4 ks .. 4 ks + 3
-  k3_u4 b[4][2];               // [n tile][substep]
-  uint32_t sb[4];              // B scale bytes (substep 0 | substep 1 << 8)
-};
-
-K3_DEV void k3g_load(K3gStep& st, const uint8_t* const* ap, const uint8_t* const* sp,
-                     const uint8_t* const* wp, const uint16_t* const* wsp, int ks, int h) {
-  const int k0 = ks * K3G_KSTEP;
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      st.alo[mt][s] = k3_ld16(ap[mt] + k0 + 64 * s + 16 * h);
-      st.ahi[mt][s] = k3_ld16(ap[mt] + k0 + 64 * s + 32 + 16 * h);
-    }
-    st.sa[mt] = *(const uint32_t*)(sp[mt] + k0 / 32);
-  }
-#pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
-#pragma unroll
-    for (int s = 0; s < 2; ++s) st.b[nt][s] = k3_ld16(wp[nt] + (size_t)(2 * ks + s) * 1024);
-    st.sb[nt] = wsp[nt][(size_t)ks * 64];
-  }
-}
-
-K3_DEV void k3g_mma(k3_v16f (&acc)[2][4], const K3gStep& st, int h) {
-#pragma unroll
-  for (int s = 0; s < 2; ++s) {
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      const k3_u4 lo = st.alo[mt][s], hi = st.ahi[mt][s];
-      const k3_v8i a = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
-                        (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-      const int sa = (int)(st.sa[mt] >> (16 * s + 8 * h));
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        const k3_u4 bv = st.b[nt][s];
-        const k3_v8i b = {(int)bv[0], (int)bv[1], (int)bv[2], (int)bv[3], 0, 0, 0, 0};
-        const int sb = (int)(st.sb[nt] >> (8 * s));
-        acc[mt][nt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, acc[mt][nt], 0, 4, 0,
-                                                                       sa, 0, sb);
-      }
-    }
-  }
-}
-
-#ifndef K3G_LDS
-#define K3G_LDS 1
-#endif
 
 // ---------------------------------------------------------------- LDS pipeline
 // Workgroup-shared operand stages filled by direct-to-LDS loads
@@ -170,12 +122,14 @@ K3_DEV void k3g_mma(k3_v16f (&acc)[2][4], const K3gStep& st, int h) {
 //             cost a third of the kernel's time);
 //   B  16 KB: block (T * 2 + s), T = 32-column tile of the workgroup (a copy of
 //             the tiled weights' 1 KB operand);
-//   SA 1 KB:  per wave 256 B: the 4 scale bytes of the step for its 32 rows
-//             (lanes 32..63 repeat lanes 0..31 into the upper 128 B);
-//   SB 1 KB:  the tiled scale pairs of the 8 column tiles (128 B each).
-// Each wave issues 10 loads per stage (its 32 rows' A slices in 4, 4 B blocks,
-// its 32 rows' A scales from half the wave, one dword per lane of B scales);
-// stages run K3G_STAGES - 1 steps ahead of the MFMAs.
+// Each wave issues 8 loads per stage (its 32 rows' A slices in 4, 4 B blocks);
+// stages run K3G_STAGES - 1 steps ahead of the MFMAs.  B scales go straight to
+// registers: a wave's 4 tiles' pairs of the next step, one 8-byte load per lane
+// (measured: as a per-stage direct-to-LDS load they cost fc1 7%).  The tile's A scales for the whole of K (128 rows x K/32 bytes) are
+// loaded once, before the first stage, into a table behind the stages (measured:
+// one 4-byte load per row and step, 32 gathered rows per instruction, cost fc1 15%).
+// The table holds KGM bytes per row: entries for K <= 3584 (KGM 112) keep two
+// workgroups per CU (2 x 80 KB of LDS); the "_w" entries (KGM 224) take K <= 7168.
 // Two stages (68 KB) and at most 256 registers per wave let two workgroups share
 // a CU, so one computes while the other waits at its step barrier (measured:
 // 3 stages at one workgroup per CU ran fc1 / fc2 at 1215 / 549 us, 2 stages at
@@ -186,17 +140,19 @@ K3_DEV void k3g_mma(k3_v16f (&acc)[2][4], const K3gStep& st, int h) {
 #ifndef K3G_WAVES_PER_EU
 #define K3G_WAVES_PER_EU 2
 #endif
-#define K3G_SA_OFF 32768
-#define K3G_SB_OFF (32768 + 1024)
-#define K3G_STAGE_BYTES (32768 + 1024 + 1024)
-#define K3G_LOADS_PER_STAGE 10
+#define K3G_STAGE_BYTES 32768
+#define K3G_LOADS_PER_STAGE 8
+#define K3G_SAT_OFF (K3G_STAGES * K3G_STAGE_BYTES)
 
 typedef __attribute__((address_space(3))) void k3g_lds_t;
 
 // The workgroup's LDS: the operand stages of the main loop, then the epilogue's
 // transposition tiles (one object shared by every caller in a kernel).
+#define K3G_EP_BYTES (4 * 64 * 272)  // the bf16 epilogue's four 64-row tiles
+template <int KGM>
 K3_DEV uint8_t* k3g_smem() {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[K3G_STAGES * K3G_STAGE_BYTES];
+  constexpr int kMain = K3G_SAT_OFF + 128 * KGM;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kMain > K3G_EP_BYTES ? kMain : K3G_EP_BYTES];
   return smem;
 }
 
@@ -211,9 +167,8 @@ K3_DEV constexpr int k3g_vmcnt(int n) {  // s_waitcnt vmcnt(n), other counters u
 // different bank groups.
 K3_DEV int k3g_aslot(int r, int c) { return 8 * r + (c ^ (r & 7)); }
 
-K3_DEV void k3g_issue_stage(uint8_t* st, const uint8_t* const* arow, const uint8_t* sarow,
-                            const uint8_t* wblk, const uint8_t* wsblk, int ks, int KT, int KS,
-                            int w, int lane) {
+K3_DEV void k3g_issue_stage(uint8_t* st, const uint8_t* const* arow, const uint8_t* wblk, int ks,
+                            int KT, int w, int lane) {
   const int k0 = ks * K3G_KSTEP;
   const int c = (lane & 7) ^ (lane >> 3);  // the chunk this lane moves (row 8 q + lane / 8)
 #pragma unroll
@@ -226,21 +181,14 @@ K3_DEV void k3g_issue_stage(uint8_t* st, const uint8_t* const* arow, const uint8
     __builtin_amdgcn_global_load_lds(wblk + ((size_t)T * KT + 2 * ks + s) * 1024 + 16 * lane,
                                      (k3g_lds_t*)(st + 16384 + (T * 2 + s) * 1024), 16, 0, 0);
   }
-  // A scales: lanes 0..31 load the dwords of rows 32 w + lane (lanes 32..63 load the
-  // same dwords again into the next 128 bytes, which nobody reads)
-  __builtin_amdgcn_global_load_lds(sarow + ks * 4, (k3g_lds_t*)(st + K3G_SA_OFF + w * 256), 4,
-                                   0, 0);
-  // B scales: dword lane of tiles 2 w + lane / 32
-  __builtin_amdgcn_global_load_lds(
-      wsblk + ((size_t)(2 * w + (lane >> 5)) * KS + ks) * 128 + 4 * (lane & 31),
-      (k3g_lds_t*)(st + K3G_SB_OFF + w * 256), 4, 0, 0);
 }
 
+template <int KGM>
 K3_DEV void k3g_lds_loop(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
                          const uint8_t* __restrict__ a_sf, const int* __restrict__ a_rows,
                          const uint8_t* __restrict__ wt, const uint16_t* __restrict__ wsf, int tile,
                          int e, int N, int K, int w, int lane, int wm, int wn) {
-  uint8_t* lds = k3g_smem();
+  uint8_t* lds = k3g_smem<KGM>();
   const int h = lane >> 5, j = lane & 31;
   const int KG = K / 32, KT = K / 64, KS = K / K3G_KSTEP, NT = N / 32;
   // this wave's loads: A rows 32 w + 8 b + lane / 8 (b < 4), scale rows 32 w + j
@@ -252,17 +200,33 @@ K3_DEV void k3g_lds_loop(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
     src = src < 0 ? 0 : src;
     arow[b] = a + (size_t)src * K;
   }
-  const int rs = tile * K3G_TILE_M + 32 * w + j;
-  int ssrc = a_rows ? a_rows[rs] : rs;
-  ssrc = ssrc < 0 ? 0 : ssrc;
-  const uint8_t* sarow = a_sf + (size_t)ssrc * KG;
   const size_t T0 = (size_t)e * NT + blockIdx.x * (K3G_TILE_N / 32);
   const uint8_t* wblk = wt + T0 * KT * 1024;
-  const uint8_t* wsblk = (const uint8_t*)wsf + T0 * KS * 128;
+  // this wave's B scale pairs: group G = T0 / 4 + wn of its 4 tiles, 8 bytes per lane
+  // per step
+  const uint2* sbp =
+      (const uint2*)wsf + ((size_t)e * (NT / 4) + blockIdx.x * (K3G_TILE_N / 128) + wn) * KS * 64 +
+      lane;
 
+  // the tile's A scales for all of K (KG <= KGM bytes per row), once
+  // (two threads per row, each one row lookup and then independent dword loads)
+  uint8_t* sat = lds + K3G_SAT_OFF;
+  {
+    const int row = threadIdx.x >> 1, KGd = KG / 4, half = (KGd + 1) >> 1;
+    const int d0 = (threadIdx.x & 1) ? half : 0, d1 = (threadIdx.x & 1) ? KGd : half;
+    const int r = tile * K3G_TILE_M + row;
+    int src = a_rows ? a_rows[r] : r;
+    src = src < 0 ? 0 : src;
+    const uint32_t* sr = (const uint32_t*)(a_sf + (size_t)src * KG);
+    uint32_t* dr = (uint32_t*)(sat + row * KGM);
+#pragma unroll 8
+    for (int d = d0; d < d1; ++d) dr[d] = sr[d];
+  }
+  uint2 sbn = sbp[0];
+  __syncthreads();  // no stage load is in flight yet
 #pragma unroll
   for (int p = 0; p < K3G_STAGES - 1; ++p)
-    if (p < KS) k3g_issue_stage(lds + p * K3G_STAGE_BYTES, arow, sarow, wblk, wsblk, p, KT, KS, w, lane);
+    if (p < KS) k3g_issue_stage(lds + p * K3G_STAGE_BYTES, arow, wblk, p, KT, w, lane);
 
   for (int ks = 0; ks < KS; ++ks) {
     // this wave's loads of step ks are done once at most the later issued stages remain
@@ -271,13 +235,15 @@ K3_DEV void k3g_lds_loop(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
     __builtin_amdgcn_s_barrier();  // every wave's loads of step ks landed; stage ks - 1 is free
                                    // (its last reads were before this barrier)
     const uint8_t* st = lds + (ks % K3G_STAGES) * K3G_STAGE_BYTES;
+    const uint2 sbc = sbn;
+    if (ks + 1 < KS) sbn = sbp[(size_t)(ks + 1) * 64];
     uint32_t sa[2], sb[4];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
-      sa[mt] = *(const uint32_t*)(st + K3G_SA_OFF + (2 * wm + mt) * 256 + 4 * j);
+      sa[mt] = *(const uint32_t*)(sat + (32 * (2 * wm + mt) + j) * KGM + 4 * ks);
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt)
-      sb[nt] = *(const uint16_t*)(st + K3G_SB_OFF + (4 * wn + nt) * 128 + 2 * lane);
+      sb[nt] = ((nt & 2 ? sbc.y : sbc.x) >> (16 * (nt & 1))) & 0xffffu;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       k3_v8i av[2];
@@ -303,8 +269,8 @@ K3_DEV void k3g_lds_loop(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
       // the next stage's loads go out behind the first substep's MFMAs, so that the
       // matrix cores start right after the barrier
       if (s == 0 && ks + K3G_STAGES - 1 < KS)
-        k3g_issue_stage(lds + ((ks + K3G_STAGES - 1) % K3G_STAGES) * K3G_STAGE_BYTES, arow, sarow,
-                        wblk, wsblk, ks + K3G_STAGES - 1, KT, KS, w, lane);
+        k3g_issue_stage(lds + ((ks + K3G_STAGES - 1) % K3G_STAGES) * K3G_STAGE_BYTES, arow, wblk,
+                        ks + K3G_STAGES - 1, KT, w, lane);
     }
   }
 }
@@ -312,6 +278,7 @@ K3_DEV void k3g_lds_loop(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
 // Accumulates the wave's 64 x 128 block; returns false when the tile is past
 // the routing tables' live count or its expert is out of range (the whole
 // workgroup exits).
+template <int KGM>
 K3_DEV bool k3g_block(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
                       const uint8_t* __restrict__ a_sf, const int* __restrict__ a_rows,
                       const uint8_t* __restrict__ wt, const uint16_t* __restrict__ wsf,
@@ -325,45 +292,13 @@ K3_DEV bool k3g_block(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
   lane = threadIdx.x & 63;
   wm = w >> 1;
   wn = w & 1;
-  const int h = lane >> 5, j = lane & 31;
-  const int KG = K / 32, KT = K / 64, KS = K / K3G_KSTEP, NT = N / 32;
-
-  const uint8_t* ap[2];
-  const uint8_t* sp[2];
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-    const int r = tile * K3G_TILE_M + 64 * wm + 32 * mt + j;
-    int src = a_rows ? a_rows[r] : r;
-    src = src < 0 ? 0 : src;
-    ap[mt] = a + (size_t)src * K;
-    sp[mt] = a_sf + (size_t)src * KG;
-  }
-  const uint8_t* wp[4];
-  const uint16_t* wsp[4];
-#pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
-    const int T = blockIdx.x * (K3G_TILE_N / 32) + 4 * wn + nt;
-    wp[nt] = wt + ((size_t)e * NT + T) * KT * 1024 + lane * 16;
-    wsp[nt] = wsf + ((size_t)e * NT + T) * KS * 64 + lane;
-  }
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
       for (int q = 0; q < 16; ++q) acc[mt][nt][q] = 0.0f;
-
-#if K3G_LDS
-  k3g_lds_loop(acc, a, a_sf, a_rows, wt, wsf, tile, e, N, K, w, lane, wm, wn);
-#else
-  K3gStep cur, nxt;
-  k3g_load(cur, ap, sp, wp, wsp, 0, h);
-  for (int ks = 0; ks < KS; ++ks) {
-    if (ks + 1 < KS) k3g_load(nxt, ap, sp, wp, wsp, ks + 1, h);
-    k3g_mma(acc, cur, h);
-    cur = nxt;
-  }
-#endif
+  k3g_lds_loop<KGM>(acc, a, a_sf, a_rows, wt, wsf, tile, e, N, K, w, lane, wm, wn);
   return true;
 }
 
@@ -378,11 +313,11 @@ K3_DEV int k3g_out_row(int wm, int mt, int q, int h) {
       const uint16_t *__restrict__ wsf, const int *__restrict__ num_tiles,                  \
       const int *__restrict__ cta_batch, int E, int N, int K
 
-extern "C" __global__ void __launch_bounds__(256, K3G_WAVES_PER_EU) kern_k3h_moe_gemm_f32(K3G_PARAMS,
-                                                                        float* __restrict__ out) {
+template <int KGM>
+K3_DEV void k3g_gemm_f32(K3G_PARAMS, float* __restrict__ out) {
   k3_v16f acc[2][4];
   int tile, e, lane, wm, wn;
-  if (!k3g_block(acc, a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch, E, N, K, tile, e, lane, wm, wn))
+  if (!k3g_block<KGM>(acc, a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch, E, N, K, tile, e, lane, wm, wn))
     return;
   const int h = lane >> 5, j = lane & 31;
 #pragma unroll
@@ -405,15 +340,15 @@ extern "C" __global__ void __launch_bounds__(256, K3G_WAVES_PER_EU) kern_k3h_moe
 #define K3G_EP_ROW 272
 #define K3G_EP_TILE (64 * K3G_EP_ROW)
 
-extern "C" __global__ void __launch_bounds__(256, K3G_WAVES_PER_EU) kern_k3h_moe_gemm_bf16(K3G_PARAMS,
-                                                                         uint16_t* __restrict__ out) {
+template <int KGM>
+K3_DEV void k3g_gemm_bf16(K3G_PARAMS, uint16_t* __restrict__ out) {
   k3_v16f acc[2][4];
   int tile, e, lane, wm, wn;
-  if (!k3g_block(acc, a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch, E, N, K, tile, e, lane, wm, wn))
+  if (!k3g_block<KGM>(acc, a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch, E, N, K, tile, e, lane, wm, wn))
     return;
   const int h = lane >> 5, j = lane & 31;
   __syncthreads();  // every wave is done with the operand stages
-  uint8_t* wl = k3g_smem() + (threadIdx.x >> 6) * K3G_EP_TILE;
+  uint8_t* wl = k3g_smem<KGM>() + (threadIdx.x >> 6) * K3G_EP_TILE;
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -438,19 +373,19 @@ extern "C" __global__ void __launch_bounds__(256, K3G_WAVES_PER_EU) kern_k3h_moe
 // e4m3 of x * 2^-e), with 16-byte payload stores and one 2-byte scale store.
 #define K3G_ACT_ROW 144
 
-extern "C" __global__ void __launch_bounds__(256, K3G_WAVES_PER_EU) kern_k3h_moe_gemm_situ_mx(
-    K3G_PARAMS, uint8_t* __restrict__ out_q, uint8_t* __restrict__ out_sf,
-    const float* __restrict__ alpha, const float* __restrict__ beta) {
+template <int KGM>
+K3_DEV void k3g_gemm_situ_mx(K3G_PARAMS, uint8_t* __restrict__ out_q, uint8_t* __restrict__ out_sf,
+                             const float* __restrict__ alpha, const float* __restrict__ beta) {
   k3_v16f acc[2][4];
   int tile, e, lane, wm, wn;
-  if (!k3g_block(acc, a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch, E, N, K, tile, e, lane, wm, wn))
+  if (!k3g_block<KGM>(acc, a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch, E, N, K, tile, e, lane, wm, wn))
     return;
   const int h = lane >> 5, j = lane & 31;
   const float al = alpha[e], be = beta[e];
   const float ial = 1.0f / al, ibe = 1.0f / be;
   const int NA = N / 2;  // activation columns
   __syncthreads();       // every wave is done with the operand stages
-  uint8_t* wl = k3g_smem() + (threadIdx.x >> 6) * (64 * K3G_ACT_ROW);
+  uint8_t* wl = k3g_smem<KGM>() + (threadIdx.x >> 6) * (64 * K3G_ACT_ROW);
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -488,3 +423,24 @@ extern "C" __global__ void __launch_bounds__(256, K3G_WAVES_PER_EU) kern_k3h_moe
   }
   *(uint16_t*)(out_sf + row * (NA / 32) + col0 / 32) = (uint16_t)sfp;
 }
+
+// Entries: K <= 3584 (A-scale table of 112 bytes per row, two workgroups per CU)
+// and, suffix _w, K <= 7168 (224 bytes per row, one workgroup per CU).
+#define K3G_ARGS a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch, E, N, K
+#define K3G_ENTRIES(SUF, KGM)                                                                    \
+  extern "C" __global__ void __launch_bounds__(256, K3G_WAVES_PER_EU)                            \
+      kern_k3h_moe_gemm_f32##SUF(K3G_PARAMS, float* __restrict__ out) {                          \
+    k3g_gemm_f32<KGM>(K3G_ARGS, out);                                                            \
+  }                                                                                              \
+  extern "C" __global__ void __launch_bounds__(256, K3G_WAVES_PER_EU)                            \
+      kern_k3h_moe_gemm_bf16##SUF(K3G_PARAMS, uint16_t* __restrict__ out) {                      \
+    k3g_gemm_bf16<KGM>(K3G_ARGS, out);                                                           \
+  }                                                                                              \
+  extern "C" __global__ void __launch_bounds__(256, K3G_WAVES_PER_EU)                            \
+      kern_k3h_moe_gemm_situ_mx##SUF(K3G_PARAMS, uint8_t* __restrict__ out_q,                    \
+                                     uint8_t* __restrict__ out_sf, const float* __restrict__ alpha, \
+                                     const float* __restrict__ beta) {                          \
+    k3g_gemm_situ_mx<KGM>(K3G_ARGS, out_q, out_sf, alpha, beta);                                 \
+  }
+K3G_ENTRIES(, 112)
+K3G_ENTRIES(_w, 224)

@@ -586,7 +586,7 @@ class Ctx:
         """E8M0 scales [experts, n, k/32] -> the tiled scale layout."""
         nbytes = experts * n * k // 32
         _dev(src, "src", U8, nbytes, align=1)
-        _dev(dst, "dst", U8, nbytes, align=2)
+        _dev(dst, "dst", U8, nbytes, align=8)
         _check(self.L.k3h_moe_sf_tile(self.h, _stream(stream), _ptr(src), _ptr(dst), experts, n, k,
                                       gated), "moe_sf_tile")
 
@@ -600,7 +600,7 @@ class Ctx:
         if a_rows is not None:
             _dev(a_rows, "a_rows", I32, rows, align=4)
         _dev(wt, "wt", U8, E * N * K // 2)
-        _dev(wsf, "wsf", U8, E * N * K // 32, align=2)
+        _dev(wsf, "wsf", U8, E * N * K // 32, align=8)
         _dev(num_tiles, "num_tiles", I32, 1, align=4)
         _dev(cta_batch, "cta_batch", I32, max_tiles, align=4)
         if epilogue == self.GEMM_F32:

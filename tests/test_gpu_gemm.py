@@ -52,15 +52,17 @@ def _w_tile_np(w, n, k, gated):
 
 
 def _sf_tile_np(wsf, n, k, gated):
+    """[E][n/128][k/128][64 lanes][4 tiles][2]: tile T = 4 G + u, byte s = block 4 ks + 2 s + h."""
     E = wsf.shape[0]
-    NT, KS = n // 32, k // 128
-    out = np.empty((E, NT, KS, 64, 2), np.uint8)
+    NG, KS = n // 128, k // 128
+    out = np.empty((E, NG, KS, 64, 4, 2), np.uint8)
     l = np.arange(64)
-    for T in range(NT):
-        r = np.array([_tile_row(T, j, n, gated) for j in l % 32])
-        for ks in range(KS):
-            for s in range(2):
-                out[:, T, ks, :, s] = wsf[:, r, 4 * ks + 2 * s + l // 32]
+    for G in range(NG):
+        for u in range(4):
+            r = np.array([_tile_row(4 * G + u, j, n, gated) for j in l % 32])
+            for ks in range(KS):
+                for s in range(2):
+                    out[:, G, ks, :, u, s] = wsf[:, r, 4 * ks + 2 * s + l // 32]
     return out
 
 
@@ -116,7 +118,7 @@ def _check_acc(got, q, sf, rows, w, wsf, cta, nt, E, N, K):
 
 
 @pytest.mark.parametrize("E,N,K,gather", [(4, 512, 1024, True), (3, 256, 3584, False),
-                                          (2, 768, 256, True)])
+                                          (2, 768, 256, True), (2, 256, 7168, True)])
 def test_gemm_f32_accumulators(ctx, E, N, K, gather):
     _case(f"gemm f32 E={E} N={N} K={K} gather={gather}")
     rows_src = 700
@@ -215,3 +217,6 @@ def test_gemm_rejects_bad_shapes(ctx):
         ctx.moe_gemm_mx(ctx.GEMM_F32, z, z, None, z, z, i, i, 1, 1, 128, 128, f)
     with pytest.raises(ValueError):  # K not a multiple of 128
         ctx.moe_gemm_mx(ctx.GEMM_F32, z, z, None, z, z, i, i, 1, 1, 256, 64, f)
+    big = torch.zeros(1 << 21, dtype=torch.uint8, device="cuda")
+    with pytest.raises(ValueError):  # K above the scale table's 7168
+        ctx.moe_gemm_mx(ctx.GEMM_F32, big, big, None, big, big, i, i, 1, 1, 256, 7296, f)
