@@ -18,7 +18,9 @@
 // evaluated as y0 = fma(x0, c, -(x1 s)), y1 = fma(x0, s, x1 c) with c, s the f32
 // roundings of cos / sin computed in double (lanes 0..31 of the wave, one pair
 // each, shared through LDS).  The sum of squares is 8 serial fmas per lane and a
-// 64-lane xor butterfly (32, 16, ..., 1).  q is [T, H, 192] contiguous, the
+// 64-lane xor butterfly (32, 16, ..., 1).  A wave's loads (latent, k_rope and
+// the first 8 q vectors per lane) are issued before the fp64 angles and the
+// barrier, so that their latency covers the angle computation.  q is [T, H, 192] contiguous, the
 // latent row [T, 576] (16-byte aligned rows).
 #include "../common/k3_dev.h"
 
@@ -56,19 +58,29 @@ extern "C" __global__ void __launch_bounds__(256) k3h_mla_rope_pack(
   const bool live = t < T;
   const int tt = live ? t : T - 1;  // loads stay in bounds; stores are predicated
 
+  // every load of the first batch goes out before the angles (fp64) and the
+  // barrier: the latent row, k_rope (8 lanes) and up to 8 q vectors per lane
+  const int nvec = H * (K3_QH / 8);  // q: H heads x 24 vectors; 16..23 are rope dims
+  const uint16_t* qrow = q + (size_t)tt * H * K3_QH;
+  const k3_u4 x = k3_ld16_nt(latent + (size_t)tt * K3_KV + 8 * l);
+  k3_u4 kr = {0u, 0u, 0u, 0u};
+  if (l < K3_ROPE / 8) kr = k3_ld16(k_rope + (size_t)tt * K3_ROPE + 8 * l);
+  k3_u4 a[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    if (64 * k < nvec) a[k] = k3_ld16_nt(qrow + 8 * min(l + 64 * k, nvec - 1));
   if (l < K3_ROPE / 2) {
     const double inv = pow((double)theta, -(double)(2 * l) / (double)K3_ROPE);
     const double ang = (double)positions[tt] * inv;
     s_cs[wv][l] = make_float2((float)cos(ang), (float)sin(ang));
   }
   // latent RMSNorm: lane l owns elements 8l .. 8l + 7
-  const k3_u4 x = k3_ld16_nt(latent + (size_t)tt * K3_KV + 8 * l);
   float sq = 0.0f;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const float a = k3_bf_lo(x[k]), b = k3_bf_hi(x[k]);
-    sq = __builtin_fmaf(a, a, sq);
-    sq = __builtin_fmaf(b, b, sq);
+    const float a0 = k3_bf_lo(x[k]), b0 = k3_bf_hi(x[k]);
+    sq = __builtin_fmaf(a0, a0, sq);
+    sq = __builtin_fmaf(b0, b0, sq);
   }
   sq += __shfl_xor(sq, 32, 64);
   sq = k3_sum32(sq);
@@ -84,20 +96,17 @@ extern "C" __global__ void __launch_bounds__(256) k3h_mla_rope_pack(
     nv[k] = k3_mul_bf2(k3_pack_bf2(k3_bf_lo(x[k]) * r, k3_bf_hi(x[k]) * r), g[k]);
   uint16_t* lrow = latent_out + (size_t)t * K3_LAT;
   k3_st16_nt(lrow + 8 * l, nv);
-  if (l < K3_ROPE / 8) {  // k_rope: 8 lanes x 8 values
-    const k3_u4 kr = k3_ld16(k_rope + (size_t)t * K3_ROPE + 8 * l);
-    k3_st16_nt(lrow + K3_KV + 8 * l, k3_rope_vec(kr, cs, 4 * l));
-  }
-  // q: H heads x 24 vectors of 8 values; vectors 16..23 of a head are the rope dims
-  const int nvec = H * (K3_QH / 8);
-  const uint16_t* qrow = q + (size_t)t * H * K3_QH;
+  if (l < K3_ROPE / 8) k3_st16_nt(lrow + K3_KV + 8 * l, k3_rope_vec(kr, cs, 4 * l));
   uint16_t* orow = q_out + (size_t)t * H * K3_QH;
   // batches of 8 vectors per lane, all loaded before the first store (indices
-  // past the row are clamped for the load and skipped for the store)
+  // past the row are clamped for the load and skipped for the store); the first
+  // batch was loaded above
   for (int w0 = 0; w0 < nvec; w0 += 64 * 8) {
-    k3_u4 a[8];
+    if (w0 > 0) {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) a[k] = k3_ld16_nt(qrow + 8 * min(w0 + l + 64 * k, nvec - 1));
+      for (int k = 0; k < 8; ++k)
+        if (w0 + 64 * k < nvec) a[k] = k3_ld16_nt(qrow + 8 * min(w0 + l + 64 * k, nvec - 1));
+    }
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const int w = w0 + l + 64 * k;
