@@ -152,6 +152,16 @@ K3_DEV void k3_mla_head_rows(const k3_mla_t* __restrict__ partial,
 #pragma unroll
   for (int k = 0; k < 3; ++k) qv[k] = k3_mla_ld4(P + 4 * (32 * (3 * sub + k) + lane));
   const float4 kv = k3_mla_ld4(P + 4 * (QU + 32 * sub + lane));
+  // Everything the stores after the barrier need is requested now, so that
+  // the slot lookup, the gammas and the rope units travel under the reductions.
+  const bool rope_lane = sub == 0 && lane < ROPE / 4;
+  float4 rv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (rope_lane) rv = k3_mla_ld4(P + 4 * (KU + lane));
+  const long long slot = live ? slot_mapping[b] : -1;
+  k3_u2 gq[3];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) gq[k] = *(const k3_u2*)(gamma_q_a + 4 * (32 * (3 * sub + k) + lane));
+  const k3_u2 gk = *(const k3_u2*)(gamma_kv_a + 4 * (32 * sub + lane));
   if (GATE && live) {
 #pragma unroll
     for (int k = 0; k < GV; ++k)
@@ -179,22 +189,15 @@ K3_DEV void k3_mla_head_rows(const k3_mla_t* __restrict__ partial,
 #pragma unroll
   for (int k = 0; k < 3; ++k) {
     const int u = 32 * (3 * sub + k) + lane;
-    const k3_u2 g = *(const k3_u2*)(gamma_q_a + 4 * u);
-    *(k3_u2*)(q_norm + (size_t)b * Q_LORA + 4 * u) = k3_norm4(qv[k], scq, g);
+    *(k3_u2*)(q_norm + (size_t)b * Q_LORA + 4 * u) = k3_norm4(qv[k], scq, gq[k]);
   }
-  const long long slot = slot_mapping[b];
   if (slot < 0) return;
   uint16_t* const rowp = slab + (slot / 64) * page_stride + layer_off + (slot % 64) * KV_A;
-  {
-    const int u = 32 * sub + lane;
-    const k3_u2 g = *(const k3_u2*)(gamma_kv_a + 4 * u);
-    *(k3_u2*)(rowp + 4 * u) = k3_norm4(kv, sck, g);
-  }
-  if (sub == 0 && lane < ROPE / 4) {  // the row's 16 rope units: a landing only
-    const float4 v = k3_mla_ld4(P + 4 * (KU + lane));
+  *(k3_u2*)(rowp + 4 * (32 * sub + lane)) = k3_norm4(kv, sck, gk);
+  if (rope_lane) {  // the row's 16 rope units: a landing only
     k3_u2 o;
-    o[0] = k3_pack_bf2(v.x, v.y);
-    o[1] = k3_pack_bf2(v.z, v.w);
+    o[0] = k3_pack_bf2(rv.x, rv.y);
+    o[1] = k3_pack_bf2(rv.z, rv.w);
     *(k3_u2*)(rowp + KV_LORA + 4 * lane) = o;
   }
 }
