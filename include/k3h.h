@@ -303,7 +303,10 @@ K3H_API int k3h_mla_rope_pack(k3h_ctx_t ctx, void* stream, const void* latent,
  *                     alpha[e], beta[e])) -> out e4m3 [.., N/2] (16-byte
  *                     aligned), out_sf E8M0 [.., N/64] (2-byte aligned),
  *                     quantised as kern_k3_moe_quant (fc1).
- * The grid is (N/256, max_tiles); tiles >= *num_tiles exit.  N % 256 == 0,
+ * Work items are (tile < min(*num_tiles, max_tiles), 256-column block); the
+ * workgroups hand them out per XCD (each XCD a contiguous share of the tiles and
+ * columns, so that its L2 holds the operands its workgroups share); the grid
+ * (N/256, rows) has enough rows for every XCD's share.  N % 256 == 0,
  * K % 128 == 0, K <= 7168; rows of padding tiles route token 0 and are
  * computed.  a_rows values (when given) must index rows of a / a_sf. */
 #define K3H_GEMM_F32 0

@@ -26,11 +26,27 @@ bool gemm_shape_ok(int E, int N, int K, int max_tiles) {
 }
 
 K3hArgs gemm_args(const void* a, const void* a_sf, const int* a_rows, const void* wt,
-                  const void* wsf, const int* num_tiles, const int* cta_batch, int E, int N, int K) {
+                  const void* wsf, const int* num_tiles, const int* cta_batch, int E, int N, int K,
+                  int max_tiles) {
   K3hArgs args;
-  args.ptr(a).ptr(a_sf).ptr(a_rows).ptr(wt).ptr(wsf).ptr(num_tiles).ptr(cta_batch).i32(E).i32(N).i32(
-      K);
+  args.ptr(a).ptr(a_sf).ptr(a_rows).ptr(wt).ptr(wsf).ptr(num_tiles).ptr(cta_batch);
+  args.i32(E).i32(N).i32(K).i32(max_tiles);
   return args;
+}
+
+// Grid rows of a GEMM launch.  The kernel hands the live (tile, column block)
+// items out per XCD (workgroups are dispatched round-robin over the 8 XCDs by
+// linear id), the XCDs forming an xt x xc grid over (tiles, column blocks) with
+// xt * xc = 8; XCD x then needs ceil(tiles / xt) * ceil(nc / xc) workgroups of
+// its own.  The grid is sized for the largest such need over every split, so it
+// covers the kernel whichever split it was built with.
+uint32_t gemm_grid_rows(int max_tiles, int nc) {
+  int64_t need = 0;
+  for (int xc = 1; xc <= 8; xc *= 2) {
+    const int64_t xt = 8 / xc;
+    need = std::max<int64_t>(need, 8 * k3h_cdiv(max_tiles, xt) * k3h_cdiv(nc, xc));
+  }
+  return (uint32_t)k3h_cdiv(need, nc);
 }
 
 bool gemm_ptrs_ok(const void* a, const void* a_sf, const int* a_rows, const void* wt,
@@ -74,7 +90,7 @@ K3H_API int k3h_moe_gemm_mx(k3h_ctx_t ctx, void* stream, int epilogue, const voi
                             const float* beta) {
   if (!ctx || !gemm_shape_ok(E, N, K, max_tiles)) return K3H_EINVAL;
   if (!gemm_ptrs_ok(a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch)) return K3H_EINVAL;
-  K3hArgs args = gemm_args(a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch, E, N, K);
+  K3hArgs args = gemm_args(a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch, E, N, K, max_tiles);
   const bool wide = K > kMaxKNarrow;
   const char* entry = nullptr;
   switch (epilogue) {
@@ -98,8 +114,9 @@ K3H_API int k3h_moe_gemm_mx(k3h_ctx_t ctx, void* stream, int epilogue, const voi
       return K3H_EINVAL;
   }
   if (max_tiles == 0) return K3H_OK;
-  return k3h_run(ctx, "k3h_moe_gemm", entry, (uint32_t)(N / kTileN), (uint32_t)max_tiles, 1,
-                 kBlock, stream, args);
+  const uint32_t rows = gemm_grid_rows(max_tiles, N / kTileN);
+  if (rows > 65535u) return K3H_EINVAL;
+  return k3h_run(ctx, "k3h_moe_gemm", entry, (uint32_t)(N / kTileN), rows, 1, kBlock, stream, args);
 }
 
 K3H_API int k3h_moe_fc1(k3h_ctx_t ctx, void* stream, const void* w13t, const void* w13_sft,

@@ -53,6 +53,8 @@
 // multiple of 8 every tile's column block x stays on XCD x % 8, so each XCD's
 // L2 holds one eighth of every expert's weights.
 #include "../common/k3_dev.h"
+#include <type_traits>
+
 #include "k3_mx.h"
 #include "k3_situ.h"
 
@@ -62,6 +64,12 @@ typedef float k3_v16f __attribute__((ext_vector_type(16)));
 #define K3G_TILE_M 128
 #define K3G_TILE_N 256
 #define K3G_KSTEP 128
+// instruction classes of __builtin_amdgcn_sched_group_barrier
+#define K3G_SG_MFMA 0x008
+#define K3G_SG_VMEM 0x010
+#define K3G_SG_VMEM_READ 0x020
+#define K3G_SG_DS_READ 0x100
+#define K3G_XCDS 8  // workgroups are dispatched round-robin over the XCDs
 
 // ---------------------------------------------------------------- layouts
 K3_DEV int k3g_row(int T, int j, int n, int gated) {
@@ -122,18 +130,20 @@ extern "C" __global__ void __launch_bounds__(256) kern_k3h_moe_sf_tile(
 //             cost a third of the kernel's time);
 //   B  16 KB: block (T * 2 + s), T = 32-column tile of the workgroup (a copy of
 //             the tiled weights' 1 KB operand);
-// Each wave issues 8 loads per stage (its 32 rows' A slices in 4, 4 B blocks);
-// stages run K3G_STAGES - 1 steps ahead of the MFMAs.  B scales go straight to
-// registers: a wave's 4 tiles' pairs of the next step, one 8-byte load per lane
-// (measured: as a per-stage direct-to-LDS load they cost fc1 7%).  The tile's A scales for the whole of K (128 rows x K/32 bytes) are
-// loaded once, before the first stage, into a table behind the stages (measured:
-// one 4-byte load per row and step, 32 gathered rows per instruction, cost fc1 15%).
-// The table holds KGM bytes per row: entries for K <= 3584 (KGM 112) keep two
-// workgroups per CU (2 x 80 KB of LDS); the "_w" entries (KGM 224) take K <= 7168.
-// Two stages (68 KB) and at most 256 registers per wave let two workgroups share
-// a CU, so one computes while the other waits at its step barrier (measured:
-// 3 stages at one workgroup per CU ran fc1 / fc2 at 1215 / 549 us, 2 stages at
-// two per CU at 832 / 466 us).
+// Each wave issues 8 loads per stage (its 32 rows' A slices in 4, 4 B blocks).
+// Two stages: the loads of step ks + 2 go out behind the barrier in the middle
+// of step ks and must land by the middle of step ks + 1.  B scales go straight
+// to registers: a wave's 4 tiles' pairs of a step, one 8-byte load per lane,
+// two steps ahead (measured: as a per-stage direct-to-LDS load they cost fc1
+// 7%).  The tile's A scales for the whole of K (128 rows x K/32 bytes) are
+// loaded once, before the first stage, into a table behind the stages
+// (measured: one 4-byte load per row and step, 32 gathered rows per
+// instruction, cost fc1 15%).  The table holds KGM bytes per row: entries for
+// K <= 3584 (KGM 112) keep two workgroups per CU (2 x 78 KB of LDS); the "_w"
+// entries (KGM 224) take K <= 7168.  Two stages and at most 256 registers per
+// wave let two workgroups share a CU, so one computes while the other waits at
+// its step barrier (measured: 3 stages at one workgroup per CU ran fc1 / fc2 at
+// 1215 / 549 us, 2 stages at two per CU at 832 / 466 us).
 #ifndef K3G_STAGES
 #define K3G_STAGES 2
 #endif
@@ -141,8 +151,8 @@ extern "C" __global__ void __launch_bounds__(256) kern_k3h_moe_sf_tile(
 #define K3G_WAVES_PER_EU 2
 #endif
 #define K3G_STAGE_BYTES 32768
-#define K3G_LOADS_PER_STAGE 8
 #define K3G_SAT_OFF (K3G_STAGES * K3G_STAGE_BYTES)
+static_assert(K3G_STAGES == 2, "the main loop alternates two stages");
 
 typedef __attribute__((address_space(3))) void k3g_lds_t;
 
@@ -156,10 +166,6 @@ K3_DEV uint8_t* k3g_smem() {
   return smem;
 }
 
-K3_DEV constexpr int k3g_vmcnt(int n) {  // s_waitcnt vmcnt(n), other counters unconstrained
-  return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8);
-}
-
 // A rows in LDS: row r of the tile's step slice (128 bytes = 8 chunks of 16) at
 // slots 8 r + (c ^ (r & 7)), c = chunk.  One load instruction moves 8 whole
 // 128-byte row slices (lane l: row 8 q + l / 8, chunk (l % 8) ^ (l / 8)), and the
@@ -167,13 +173,13 @@ K3_DEV constexpr int k3g_vmcnt(int n) {  // s_waitcnt vmcnt(n), other counters u
 // different bank groups.
 K3_DEV int k3g_aslot(int r, int c) { return 8 * r + (c ^ (r & 7)); }
 
-K3_DEV void k3g_issue_stage(uint8_t* st, const uint8_t* const* arow, const uint8_t* wblk, int ks,
-                            int KT, int w, int lane) {
+K3_DEV void k3g_issue_stage(uint8_t* st, const uint8_t* a, const uint32_t* arow,
+                            const uint8_t* wblk, int ks, int KT, int w, int lane) {
   const int k0 = ks * K3G_KSTEP;
   const int c = (lane & 7) ^ (lane >> 3);  // the chunk this lane moves (row 8 q + lane / 8)
 #pragma unroll
   for (int b = 0; b < 4; ++b)  // rows 32 w + 8 b .. + 8 of the tile
-    __builtin_amdgcn_global_load_lds(arow[b] + k0 + 16 * c,
+    __builtin_amdgcn_global_load_lds(a + arow[b] + k0 + 16 * c,
                                      (k3g_lds_t*)(st + (4 * w + b) * 1024), 16, 0, 0);
 #pragma unroll
   for (int b = 0; b < 4; ++b) {  // B blocks: tiles 2 w, 2 w + 1, both substeps
@@ -187,25 +193,26 @@ template <int KGM>
 K3_DEV void k3g_lds_loop(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
                          const uint8_t* __restrict__ a_sf, const int* __restrict__ a_rows,
                          const uint8_t* __restrict__ wt, const uint16_t* __restrict__ wsf, int tile,
-                         int e, int N, int K, int w, int lane, int wm, int wn) {
+                         int cb, int e, int N, int K, int w, int lane, int wm, int wn) {
   uint8_t* lds = k3g_smem<KGM>();
   const int h = lane >> 5, j = lane & 31;
   const int KG = K / 32, KT = K / 64, KS = K / K3G_KSTEP, NT = N / 32;
   // this wave's loads: A rows 32 w + 8 b + lane / 8 (b < 4), scale rows 32 w + j
-  const uint8_t* arow[4];
+  // (byte offsets from a: every activation row offset fits in 32 bits, rows * K < 2^32)
+  uint32_t arow[4];
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
     const int r = tile * K3G_TILE_M + 32 * w + 8 * b + (lane >> 3);
     int src = a_rows ? a_rows[r] : r;
     src = src < 0 ? 0 : src;
-    arow[b] = a + (size_t)src * K;
+    arow[b] = (uint32_t)src * (uint32_t)K;
   }
-  const size_t T0 = (size_t)e * NT + blockIdx.x * (K3G_TILE_N / 32);
+  const size_t T0 = (size_t)e * NT + cb * (K3G_TILE_N / 32);
   const uint8_t* wblk = wt + T0 * KT * 1024;
   // this wave's B scale pairs: group G = T0 / 4 + wn of its 4 tiles, 8 bytes per lane
   // per step
   const uint2* sbp =
-      (const uint2*)wsf + ((size_t)e * (NT / 4) + blockIdx.x * (K3G_TILE_N / 128) + wn) * KS * 64 +
+      (const uint2*)wsf + ((size_t)e * (NT / 4) + cb * (K3G_TILE_N / 128) + wn) * KS * 64 +
       lane;
 
   // the tile's A scales for all of K (KG <= KGM bytes per row), once
@@ -222,70 +229,160 @@ K3_DEV void k3g_lds_loop(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
 #pragma unroll 8
     for (int d = d0; d < d1; ++d) dr[d] = sr[d];
   }
-  uint2 sbn = sbp[0];
+  uint2 sbc = sbp[0];                               // B scale pairs of the current step
+  uint2 sbq = KS > 1 ? sbp[64] : make_uint2(0, 0);  // and of the next one
   __syncthreads();  // no stage load is in flight yet
-#pragma unroll
-  for (int p = 0; p < K3G_STAGES - 1; ++p)
-    if (p < KS) k3g_issue_stage(lds + p * K3G_STAGE_BYTES, arow, wblk, p, KT, w, lane);
+  k3g_issue_stage(lds, a, arow, wblk, 0, KT, w, lane);
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_s_barrier();  // stage 0 landed for every wave
+  if (KS > 1) k3g_issue_stage(lds + K3G_STAGE_BYTES, a, arow, wblk, 1, KT, w, lane);
 
-  for (int ks = 0; ks < KS; ++ks) {
-    // this wave's loads of step ks are done once at most the later issued stages remain
-    if (ks + 1 < KS) __builtin_amdgcn_s_waitcnt(k3g_vmcnt(K3G_LOADS_PER_STAGE * (K3G_STAGES - 2)));
-    else __builtin_amdgcn_s_waitcnt(k3g_vmcnt(0));
-    __builtin_amdgcn_s_barrier();  // every wave's loads of step ks landed; stage ks - 1 is free
-                                   // (its last reads were before this barrier)
-    const uint8_t* st = lds + (ks % K3G_STAGES) * K3G_STAGE_BYTES;
-    const uint2 sbc = sbn;
-    if (ks + 1 < KS) sbn = sbp[(size_t)(ks + 1) * 64];
-    uint32_t sa[2], sb[4];
+  // Operand reads.  The A operand of substep s: row r = 32 (2 wm + mt) + j, chunks
+  // 4 s + h and 4 s + 2 + h of its 128-byte slice; the B operand: 1 KB block
+  // (T, s) in lane order.
+  auto rd_a = [&](const uint8_t* st, int s, int mt) -> k3_v8i {
+    const int r = 32 * (2 * wm + mt) + j;
+    const k3_u4 lo = *(const k3_u4*)(st + 16 * k3g_aslot(r, 4 * s + h));
+    const k3_u4 hi = *(const k3_u4*)(st + 16 * k3g_aslot(r, 4 * s + 2 + h));
+    return (k3_v8i){(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
+                    (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+  };
+  auto rd_b = [&](const uint8_t* st, int s, int nt) -> k3_u4 {
+    return *(const k3_u4*)(st + 16384 + ((4 * wn + nt) * 2 + s) * 1024 + 16 * lane);
+  };
+  auto rd_sa = [&](int ks, int mt) -> uint32_t {
+    return *(const uint32_t*)(sat + (32 * (2 * wm + mt) + j) * KGM + 4 * ks);
+  };
+  auto mfma = [&](int mt, int nt, const k3_v8i& av, const k3_u4& bv, uint32_t sa, uint32_t sb,
+                  int s) {
+    const k3_v8i b = {(int)bv[0], (int)bv[1], (int)bv[2], (int)bv[3], 0, 0, 0, 0};
+    acc[mt][nt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+        av, b, acc[mt][nt], 0, 4, 0, (int)(sa >> (16 * s + 8 * h)), 0, (int)(sb >> (8 * s)));
+  };
+
+  // Software pipeline: the operands of the next substep are read from LDS behind
+  // the current substep's MFMAs (A double-buffered, each B operand re-read as soon
+  // as its two MFMAs are issued).  The barrier sits in the middle of the step:
+  // there every wave's loads of the next stage have landed and every wave's reads
+  // of the current stage are done, so the stage is refilled with step ks + 2.
+  // The step body is instantiated branch-free for the steady state (MORE: a next
+  // step exists; ISSUE: step ks + 2 exists) and peeled for the last two steps.
+  k3_v8i a0[2], a1[2];
+  k3_u4 bv[4];
+  uint32_t sa[2];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-      sa[mt] = *(const uint32_t*)(sat + (32 * (2 * wm + mt) + j) * KGM + 4 * ks);
+  for (int mt = 0; mt < 2; ++mt) a0[mt] = rd_a(lds, 0, mt);
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) bv[nt] = rd_b(lds, 0, nt);
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) sa[mt] = rd_sa(0, mt);
+
+  auto step = [&](int ks, auto more_c, auto issue_c) {
+    constexpr bool MORE = decltype(more_c)::value, ISSUE = decltype(issue_c)::value;
+    uint8_t* st = lds + (ks & 1) * K3G_STAGE_BYTES;
+    const uint8_t* sn = lds + ((ks + 1) & 1) * K3G_STAGE_BYTES;
+    uint32_t sb[4], san[2];
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt)
       sb[nt] = ((nt & 2 ? sbc.y : sbc.x) >> (16 * (nt & 1))) & 0xffffu;
+    // substep 0: A of substep 1 requested first, each B operand re-read behind its pair
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      k3_v8i av[2];
+    for (int mt = 0; mt < 2; ++mt) a1[mt] = rd_a(st, 1, mt);
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const int r = 32 * (2 * wm + mt) + j;
-        const k3_u4 lo = *(const k3_u4*)(st + 16 * k3g_aslot(r, 4 * s + h));
-        const k3_u4 hi = *(const k3_u4*)(st + 16 * k3g_aslot(r, 4 * s + 2 + h));
-        av[mt] = (k3_v8i){(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
-                          (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-      }
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        const int T = 4 * wn + nt;
-        const k3_u4 bv = *(const k3_u4*)(st + 16384 + (T * 2 + s) * 1024 + 16 * lane);
-        const k3_v8i b = {(int)bv[0], (int)bv[1], (int)bv[2], (int)bv[3], 0, 0, 0, 0};
-        const int sbv = (int)(sb[nt] >> (8 * s));
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-          acc[mt][nt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-              av[mt], b, acc[mt][nt], 0, 4, 0, (int)(sa[mt] >> (16 * s + 8 * h)), 0, sbv);
-      }
-      // the next stage's loads go out behind the first substep's MFMAs, so that the
-      // matrix cores start right after the barrier
-      if (s == 0 && ks + K3G_STAGES - 1 < KS)
-        k3g_issue_stage(lds + ((ks + K3G_STAGES - 1) % K3G_STAGES) * K3G_STAGE_BYTES, arow, wblk,
-                        ks + K3G_STAGES - 1, KT, w, lane);
+    for (int nt = 0; nt < 4; ++nt) {
+      mfma(0, nt, a0[0], bv[nt], sa[0], sb[nt], 0);
+      mfma(1, nt, a0[1], bv[nt], sa[1], sb[nt], 0);
+      bv[nt] = rd_b(st, 1, nt);
     }
-  }
+    __builtin_amdgcn_sched_group_barrier(K3G_SG_DS_READ, 4, 0);
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      __builtin_amdgcn_sched_group_barrier(K3G_SG_MFMA, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(K3G_SG_DS_READ, 1, 0);
+    }
+    if constexpr (MORE) {
+      __builtin_amdgcn_s_waitcnt(0);  // this wave: stage ks + 1 landed, its reads of stage ks done
+      __builtin_amdgcn_s_barrier();   // every wave
+      sbc = sbq;
+      if constexpr (ISSUE) sbq = sbp[(size_t)(ks + 2) * 64];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) a0[mt] = rd_a(sn, 0, mt);
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) san[mt] = rd_sa(ks + 1, mt);
+    }
+    // substep 1; the next step's operands are read behind it, and stage ks is
+    // refilled with step ks + 2 behind its first MFMA pair
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      mfma(0, nt, a1[0], bv[nt], sa[0], sb[nt], 1);
+      mfma(1, nt, a1[1], bv[nt], sa[1], sb[nt], 1);
+      if constexpr (MORE) bv[nt] = rd_b(sn, 0, nt);
+      if constexpr (ISSUE)
+        if (nt == 0) k3g_issue_stage(st, a, arow, wblk, ks + 2, KT, w, lane);
+    }
+    if constexpr (MORE) {
+      sa[0] = san[0];
+      sa[1] = san[1];
+      __builtin_amdgcn_sched_group_barrier(K3G_SG_VMEM_READ, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(K3G_SG_DS_READ, 6, 1);
+      __builtin_amdgcn_sched_group_barrier(K3G_SG_MFMA, 2, 1);
+      __builtin_amdgcn_sched_group_barrier(K3G_SG_DS_READ, 1, 1);
+      if constexpr (ISSUE) __builtin_amdgcn_sched_group_barrier(K3G_SG_VMEM, 8, 1);
+      __builtin_amdgcn_sched_group_barrier(K3G_SG_MFMA, 2, 1);
+      __builtin_amdgcn_sched_group_barrier(K3G_SG_DS_READ, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(K3G_SG_MFMA, 2, 1);
+      __builtin_amdgcn_sched_group_barrier(K3G_SG_DS_READ, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(K3G_SG_MFMA, 2, 1);
+      __builtin_amdgcn_sched_group_barrier(K3G_SG_DS_READ, 1, 1);
+    }
+  };
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  int ks = 0;
+  for (; ks + 2 < KS; ++ks) step(ks, T_{}, T_{});
+  if (ks + 1 < KS) step(ks++, T_{}, F_{});
+  step(ks, F_{}, F_{});
 }
 
-// Accumulates the wave's 64 x 128 block; returns false when the tile is past
-// the routing tables' live count or its expert is out of range (the whole
-// workgroup exits).
+// Work item of this workgroup.  The grid is (column blocks, max route tiles);
+// only the live tiles' items (tile < *num_tiles) are work.  Workgroups are
+// dispatched round-robin over the 8 XCDs by linear id, so items are handed out
+// per XCD: the XCDs form a K3G_XT x K3G_XC grid over (live tiles, column
+// blocks), XCD x taking tile part x / K3G_XC and column part x % K3G_XC in
+// tile-major order.  A route tile's A rows are then fetched by K3G_XC XCDs
+// and an expert's weights by about K3G_XT (each L2 keeps the operands its
+// concurrent workgroups share).  Returns false for a workgroup with no item.
+#ifndef K3G_XC
+#define K3G_XC 2  // measured best of 1, 2, 4, 8 for fc1 and fc2
+#endif
+#define K3G_XT (K3G_XCDS / K3G_XC)
+K3_DEV bool k3g_item(const int* __restrict__ num_tiles, int max_tiles, int& tile, int& cb) {
+  const int nc = gridDim.x;
+  int live = *num_tiles;
+  live = live < max_tiles ? live : max_tiles;
+  const int i = blockIdx.y * nc + blockIdx.x;
+  const int x = i % K3G_XCDS, slot = i / K3G_XCDS;
+  const int xt = x / K3G_XC, xc = x % K3G_XC;
+  // this XCD's tile range [t0, t0 + nt) and column range [c0, c0 + ncx)
+  const int tq = live / K3G_XT, tr = live % K3G_XT;
+  const int nt = tq + (xt < tr ? 1 : 0), t0 = xt * tq + (xt < tr ? xt : tr);
+  const int cq = nc / K3G_XC, cr = nc % K3G_XC;
+  const int ncx = cq + (xc < cr ? 1 : 0), c0 = xc * cq + (xc < cr ? xc : cr);
+  if (slot >= nt * ncx) return false;
+  const int ti = slot / ncx;
+  tile = t0 + ti;
+  cb = c0 + (slot - ti * ncx);
+  return true;
+}
+
+// Accumulates the wave's 64 x 128 block of work item (tile, cb); returns false
+// when the tile's expert is out of range (the whole workgroup skips the item).
 template <int KGM>
 K3_DEV bool k3g_block(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
                       const uint8_t* __restrict__ a_sf, const int* __restrict__ a_rows,
                       const uint8_t* __restrict__ wt, const uint16_t* __restrict__ wsf,
-                      const int* __restrict__ num_tiles, const int* __restrict__ cta_batch, int E,
-                      int N, int K, int& tile, int& e, int& lane, int& wm, int& wn) {
-  tile = blockIdx.y;
-  if (tile >= *num_tiles) return false;
+                      const int* __restrict__ cta_batch, int E, int N, int K, int tile, int cb,
+                      int& e, int& lane, int& wm, int& wn) {
   e = cta_batch[tile];
   if (e < 0 || e >= E) return false;
   const int w = threadIdx.x >> 6;
@@ -298,8 +395,24 @@ K3_DEV bool k3g_block(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
     for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
       for (int q = 0; q < 16; ++q) acc[mt][nt][q] = 0.0f;
-  k3g_lds_loop<KGM>(acc, a, a_sf, a_rows, wt, wsf, tile, e, N, K, w, lane, wm, wn);
+  k3g_lds_loop<KGM>(acc, a, a_sf, a_rows, wt, wsf, tile, cb, e, N, K, w, lane, wm, wn);
   return true;
+}
+
+// Runs the workgroup's item (if any): accumulates it and hands it to the
+// epilogue epi(acc, tile, cb, e, lane, wm, wn).
+template <int KGM, class Epi>
+K3_DEV void k3g_items(const uint8_t* __restrict__ a, const uint8_t* __restrict__ a_sf,
+                      const int* __restrict__ a_rows, const uint8_t* __restrict__ wt,
+                      const uint16_t* __restrict__ wsf, const int* __restrict__ num_tiles,
+                      const int* __restrict__ cta_batch, int E, int N, int K, int max_tiles,
+                      Epi&& epi) {
+  int tile, cb, e, lane, wm, wn;
+  if (!k3g_item(num_tiles, max_tiles, tile, cb)) return;
+  k3_v16f acc[2][4];
+  if (!k3g_block<KGM>(acc, a, a_sf, a_rows, wt, wsf, cta_batch, E, N, K, tile, cb, e, lane, wm, wn))
+    return;
+  epi(acc, tile, cb, e, lane, wm, wn);
 }
 
 // Row of accumulator register q of m tile mt, within the route tile.
@@ -311,26 +424,25 @@ K3_DEV int k3g_out_row(int wm, int mt, int q, int h) {
   const uint8_t *__restrict__ a, const uint8_t *__restrict__ a_sf,                          \
       const int *__restrict__ a_rows, const uint8_t *__restrict__ wt,                       \
       const uint16_t *__restrict__ wsf, const int *__restrict__ num_tiles,                  \
-      const int *__restrict__ cta_batch, int E, int N, int K
+      const int *__restrict__ cta_batch, int E, int N, int K, int max_tiles
 
 template <int KGM>
 K3_DEV void k3g_gemm_f32(K3G_PARAMS, float* __restrict__ out) {
-  k3_v16f acc[2][4];
-  int tile, e, lane, wm, wn;
-  if (!k3g_block<KGM>(acc, a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch, E, N, K, tile, e, lane, wm, wn))
-    return;
-  const int h = lane >> 5, j = lane & 31;
+  k3g_items<KGM>(a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch, E, N, K, max_tiles,
+                 [&](k3_v16f(&acc)[2][4], int tile, int cb, int e, int lane, int wm, int wn) {
+    const int h = lane >> 5, j = lane & 31;
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      const int col = blockIdx.x * K3G_TILE_N + 128 * wn + 32 * nt + j;
+      for (int nt = 0; nt < 4; ++nt) {
+        const int col = cb * K3G_TILE_N + 128 * wn + 32 * nt + j;
 #pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        const size_t row = (size_t)tile * K3G_TILE_M + k3g_out_row(wm, mt, q, h);
-        out[row * N + col] = acc[mt][nt][q];
+        for (int q = 0; q < 16; ++q) {
+          const size_t row = (size_t)tile * K3G_TILE_M + k3g_out_row(wm, mt, q, h);
+          out[row * N + col] = acc[mt][nt][q];
+        }
       }
-    }
+  });
 }
 
 // Epilogue transposition: each wave writes its 64 x 128 block (bf16) to its own
@@ -342,28 +454,28 @@ K3_DEV void k3g_gemm_f32(K3G_PARAMS, float* __restrict__ out) {
 
 template <int KGM>
 K3_DEV void k3g_gemm_bf16(K3G_PARAMS, uint16_t* __restrict__ out) {
-  k3_v16f acc[2][4];
-  int tile, e, lane, wm, wn;
-  if (!k3g_block<KGM>(acc, a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch, E, N, K, tile, e, lane, wm, wn))
-    return;
-  const int h = lane >> 5, j = lane & 31;
-  __syncthreads();  // every wave is done with the operand stages
-  uint8_t* wl = k3g_smem<KGM>() + (threadIdx.x >> 6) * K3G_EP_TILE;
+  k3g_items<KGM>(a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch, E, N, K, max_tiles,
+                 [&](k3_v16f(&acc)[2][4], int tile, int cb, int e, int lane, int wm, int wn) {
+    const int h = lane >> 5, j = lane & 31;
+    __syncthreads();  // every wave is done with the operand stages
+    uint8_t* wl = k3g_smem<KGM>() + (threadIdx.x >> 6) * K3G_EP_TILE;
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
+      for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        const int r = 32 * mt + 8 * (q >> 2) + 4 * h + (q & 3);
-        *(uint16_t*)(wl + r * K3G_EP_ROW + 2 * (32 * nt + j)) =
-            (uint16_t)k3_pack_bf2(acc[mt][nt][q], 0.0f);
-      }
-  __syncthreads();
-  uint16_t* orow = out + ((size_t)tile * K3G_TILE_M + 64 * wm + lane) * N + blockIdx.x * K3G_TILE_N +
-                   128 * wn;
+        for (int q = 0; q < 16; ++q) {
+          const int r = 32 * mt + 8 * (q >> 2) + 4 * h + (q & 3);
+          *(uint16_t*)(wl + r * K3G_EP_ROW + 2 * (32 * nt + j)) =
+              (uint16_t)k3_pack_bf2(acc[mt][nt][q], 0.0f);
+        }
+    __syncthreads();
+    uint16_t* orow = out + ((size_t)tile * K3G_TILE_M + 64 * wm + lane) * N + cb * K3G_TILE_N +
+                     128 * wn;
 #pragma unroll
-  for (int c = 0; c < 16; ++c) k3_st16(orow + 8 * c, *(const k3_u4*)(wl + lane * K3G_EP_ROW + 16 * c));
+    for (int c = 0; c < 16; ++c)
+      k3_st16(orow + 8 * c, *(const k3_u4*)(wl + lane * K3G_EP_ROW + 16 * c));
+  });
 }
 
 // fc1 epilogue: the activation of the wave's 64 rows x 64 activation columns
@@ -376,57 +488,56 @@ K3_DEV void k3g_gemm_bf16(K3G_PARAMS, uint16_t* __restrict__ out) {
 template <int KGM>
 K3_DEV void k3g_gemm_situ_mx(K3G_PARAMS, uint8_t* __restrict__ out_q, uint8_t* __restrict__ out_sf,
                              const float* __restrict__ alpha, const float* __restrict__ beta) {
-  k3_v16f acc[2][4];
-  int tile, e, lane, wm, wn;
-  if (!k3g_block<KGM>(acc, a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch, E, N, K, tile, e, lane, wm, wn))
-    return;
-  const int h = lane >> 5, j = lane & 31;
-  const float al = alpha[e], be = beta[e];
-  const float ial = 1.0f / al, ibe = 1.0f / be;
-  const int NA = N / 2;  // activation columns
-  __syncthreads();       // every wave is done with the operand stages
-  uint8_t* wl = k3g_smem<KGM>() + (threadIdx.x >> 6) * (64 * K3G_ACT_ROW);
+  k3g_items<KGM>(a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch, E, N, K, max_tiles,
+                 [&](k3_v16f(&acc)[2][4], int tile, int cb, int e, int lane, int wm, int wn) {
+    const int h = lane >> 5, j = lane & 31;
+    const float al = alpha[e], be = beta[e];
+    const float ial = 1.0f / al, ibe = 1.0f / be;
+    const int NA = N / 2;  // activation columns
+    __syncthreads();       // every wave is done with the operand stages
+    uint8_t* wl = k3g_smem<KGM>() + (threadIdx.x >> 6) * (64 * K3G_ACT_ROW);
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-    for (int p = 0; p < 2; ++p)
+      for (int p = 0; p < 2; ++p)
 #pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        // logical tiles 4 wn + 2 p (up) and 4 wn + 2 p + 1 (gate): activation columns 32 p + j
-        const float u = k3_land(acc[mt][2 * p][q]);
-        const float g = k3_land(acc[mt][2 * p + 1][q]);
-        const int r = 32 * mt + 8 * (q >> 2) + 4 * h + (q & 3);
-        *(uint16_t*)(wl + r * K3G_ACT_ROW + 2 * (32 * p + j)) =
-            (uint16_t)k3_pack_bf2(k3_situ_gate_a(g, al, ial) * k3_situ_up_b(u, be, ibe), 0.0f);
+        for (int q = 0; q < 16; ++q) {
+          // logical tiles 4 wn + 2 p (up) and 4 wn + 2 p + 1 (gate): activation columns 32 p + j
+          const float u = k3_land(acc[mt][2 * p][q]);
+          const float g = k3_land(acc[mt][2 * p + 1][q]);
+          const int r = 32 * mt + 8 * (q >> 2) + 4 * h + (q & 3);
+          *(uint16_t*)(wl + r * K3G_ACT_ROW + 2 * (32 * p + j)) =
+              (uint16_t)k3_pack_bf2(k3_situ_gate_a(g, al, ial) * k3_situ_up_b(u, be, ibe), 0.0f);
+        }
+    __syncthreads();
+    const size_t row = (size_t)tile * K3G_TILE_M + 64 * wm + lane;
+    const int col0 = 64 * (2 * cb + wn);  // this wave's first activation column
+    uint32_t sfp = 0;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      k3_u4 v[4];
+      uint32_t m = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[i] = *(const k3_u4*)(wl + lane * K3G_ACT_ROW + 64 * c + 16 * i);
+        const uint32_t mi = k3_vec_absmax_bits(v[i]);
+        m = m > mi ? m : mi;
       }
-  __syncthreads();
-  const size_t row = (size_t)tile * K3G_TILE_M + 64 * wm + lane;
-  const int col0 = 64 * (2 * blockIdx.x + wn);  // this wave's first activation column
-  uint32_t sfp = 0;
-#pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    k3_u4 v[4];
-    uint32_t m = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[i] = *(const k3_u4*)(wl + lane * K3G_ACT_ROW + 64 * c + 16 * i);
-      const uint32_t mi = k3_vec_absmax_bits(v[i]);
-      m = m > mi ? m : mi;
+      const int ex = k3_e8m0_exp(m);
+      const k3_u2 q0 = k3_vec_to_e4m3(v[0], ex), q1 = k3_vec_to_e4m3(v[1], ex);
+      const k3_u2 q2 = k3_vec_to_e4m3(v[2], ex), q3 = k3_vec_to_e4m3(v[3], ex);
+      uint8_t* o = out_q + row * NA + col0 + 32 * c;
+      k3_st16(o, (k3_u4){q0[0], q0[1], q1[0], q1[1]});
+      k3_st16(o + 16, (k3_u4){q2[0], q2[1], q3[0], q3[1]});
+      sfp |= (uint32_t)(ex + 127) << (8 * c);
     }
-    const int ex = k3_e8m0_exp(m);
-    const k3_u2 q0 = k3_vec_to_e4m3(v[0], ex), q1 = k3_vec_to_e4m3(v[1], ex);
-    const k3_u2 q2 = k3_vec_to_e4m3(v[2], ex), q3 = k3_vec_to_e4m3(v[3], ex);
-    uint8_t* o = out_q + row * NA + col0 + 32 * c;
-    k3_st16(o, (k3_u4){q0[0], q0[1], q1[0], q1[1]});
-    k3_st16(o + 16, (k3_u4){q2[0], q2[1], q3[0], q3[1]});
-    sfp |= (uint32_t)(ex + 127) << (8 * c);
-  }
-  *(uint16_t*)(out_sf + row * (NA / 32) + col0 / 32) = (uint16_t)sfp;
+    *(uint16_t*)(out_sf + row * (NA / 32) + col0 / 32) = (uint16_t)sfp;
+  });
 }
 
 // Entries: K <= 3584 (A-scale table of 112 bytes per row, two workgroups per CU)
 // and, suffix _w, K <= 7168 (224 bytes per row, one workgroup per CU).
-#define K3G_ARGS a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch, E, N, K
+#define K3G_ARGS a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch, E, N, K, max_tiles
 #define K3G_ENTRIES(SUF, KGM)                                                                    \
   extern "C" __global__ void __launch_bounds__(256, K3G_WAVES_PER_EU)                            \
       kern_k3h_moe_gemm_f32##SUF(K3G_PARAMS, float* __restrict__ out) {                          \
@@ -438,8 +549,9 @@ K3_DEV void k3g_gemm_situ_mx(K3G_PARAMS, uint8_t* __restrict__ out_q, uint8_t* _
   }                                                                                              \
   extern "C" __global__ void __launch_bounds__(256, K3G_WAVES_PER_EU)                            \
       kern_k3h_moe_gemm_situ_mx##SUF(K3G_PARAMS, uint8_t* __restrict__ out_q,                    \
-                                     uint8_t* __restrict__ out_sf, const float* __restrict__ alpha, \
-                                     const float* __restrict__ beta) {                          \
+                                     uint8_t* __restrict__ out_sf,                               \
+                                     const float* __restrict__ alpha,                            \
+                                     const float* __restrict__ beta) {                           \
     k3g_gemm_situ_mx<KGM>(K3G_ARGS, out_q, out_sf, alpha, beta);                                 \
   }
 K3G_ENTRIES(, 112)
