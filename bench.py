@@ -115,11 +115,42 @@ def copy_ceiling(ctx, rows: int, reps: int) -> float:
     return gbs
 
 
-def bench_ops(ctx, reps: int, out_path: str | None) -> list:
+def cpu_timer(budget_s: float):
+    """Times one oracle call (the checker, run as a reported baseline): one untimed
+    call, then up to 3 timed calls within `budget_s`; returns the median in s."""
+    def run(fn):
+        t0 = time.perf_counter()
+        fn()
+        first = time.perf_counter() - t0
+        times = []
+        while len(times) < 3 and (not times or sum(times) + first < budget_s):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return sorted(times)[len(times) // 2]
+    return run
+
+
+def bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0) -> list:
     """Every op at its BASELINE config shape: 5 warm-up launches, then `reps`
     launches each between two HIP events on the launch stream, with a 512 MB
-    cache-flush write between launches (outside the events); median, p10, p90."""
+    cache-flush write between launches (outside the events); median, p10, p90.
+    With cpu_budget > 0, the rows of BASELINE configs 1-5 also time the C oracle
+    (OpenMP over the host cores) on host copies of the same inputs."""
+    import numpy as np
     import torch
+    O = None
+    if cpu_budget > 0:
+        sys.path.insert(0, os.path.join(REPO, "oracle"))
+        import oracle as O
+        cpu_run = cpu_timer(cpu_budget)
+        log(f"CPU oracle column: {O.num_threads()} OpenMP threads of {os.cpu_count()} hardware threads")
+
+    def h(t):
+        """Host copy: bf16 tensors as uint16 bit patterns, others as their numpy dtype."""
+        if t.dtype == torch.bfloat16:
+            return np.ascontiguousarray(t.cpu().view(torch.int16).numpy().view(np.uint16))
+        return np.ascontiguousarray(t.cpu().numpy())
     s = torch.cuda.current_stream()
     flush = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
     g = torch.Generator(device="cuda")
@@ -146,16 +177,23 @@ def bench_ops(ctx, reps: int, out_path: str | None) -> list:
 
     rows = []
 
-    def add(op, kernel, shape, nbytes, t, note=""):
+    def add(op, kernel, shape, nbytes, t, note="", cpu=None):
         us, p10, p90 = t
         gbs = nbytes / (us * 1e-6) / 1e9
-        rows.append({"op": op, "kernel": kernel, "shape": shape, "bytes": int(nbytes),
-                     "launches": 5 + reps,
-                     "us": round(us, 2), "us_p10": round(p10, 2), "us_p90": round(p90, 2),
-                     "gbs": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1),
-                     "note": note})
+        row = {"op": op, "kernel": kernel, "shape": shape, "bytes": int(nbytes),
+               "launches": 5 + reps,
+               "us": round(us, 2), "us_p10": round(p10, 2), "us_p90": round(p90, 2),
+               "gbs": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1),
+               "note": note}
+        cpu_txt = ""
+        if cpu is not None and O is not None:
+            sec = cpu_run(cpu)
+            row.update({"cpu_ms": round(sec * 1e3, 2), "cpu_gbs": round(nbytes / sec / 1e9, 2),
+                        "cpu_threads": O.num_threads()})
+            cpu_txt = f" | CPU {sec * 1e3:8.1f} ms {nbytes / sec / 1e9:6.2f} GB/s"
+        rows.append(row)
         log(f"{op:42s} {us:8.2f} us (p10 {p10:7.2f}, p90 {p90:7.2f}) {gbs:7.0f} GB/s "
-            f"{100 * gbs / PEAK_GBS:5.1f}%  {note}")
+            f"{100 * gbs / PEAK_GBS:5.1f}%{cpu_txt}  {note}")
 
     T = 16384
     # copy ceiling
@@ -171,20 +209,27 @@ def bench_ops(ctx, reps: int, out_path: str | None) -> list:
     sw = torch.zeros(H, dtype=torch.float32, device="cuda")
     add("residual add + RMSNorm (cfg 1)", "kern_k3_land_add_attnres_rms", f"{B1}x{H}",
         4 * B1 * H * 2 + H * 2,
-        timed(lambda: ctx.land_add_attnres_rms(p1, r1, None, sw, g1, o1, n1, 0, 0, B1, eps=1e-6, stream=s)))
+        timed(lambda: ctx.land_add_attnres_rms(p1, r1, None, sw, g1, o1, n1, 0, 0, B1, eps=1e-6, stream=s)),
+        cpu=O and (lambda a=(h(p1), h(r1), h(sw), h(g1)):
+                   O.land_add_attnres_rms(a[0], a[1], None, a[2], a[3], 0, 0, B1, eps=1e-6)))
     # config 2: fused, and the standalone quantisers at the same shape
     x, res, gm = make_inputs(T)
     ro = torch.empty_like(x)
     q = torch.empty((T, H), dtype=torch.uint8, device="cuda")
     sf = torch.empty((T, H // 32), dtype=torch.uint8, device="cuda")
     add("residual+RMSNorm+MXFP8 (cfg 2)", "k3h_residual_rms_mxfp8", f"{T}x{H}", algo_bytes(T),
-        timed(lambda: ctx.residual_rms_mxfp8(x, res, gm, ro, q, sf, None, eps=1e-6, B=T, stream=s)))
+        timed(lambda: ctx.residual_rms_mxfp8(x, res, gm, ro, q, sf, None, eps=1e-6, B=T, stream=s)),
+        cpu=O and (lambda a=(h(x), h(res), h(gm)):
+                   O.residual_rms_mxfp8(a[0], a[1], a[2], T, 1e-6, want_normed=False)))
+    xh = h(x) if O else None
     add("MXFP8 quant alone", "kern_k3_moe_quant", f"{T}x{H}", T * H * 2 + T * H + T * H // 32,
-        timed(lambda: ctx.moe_quant(x, q, sf, T, H, stream=s)))
+        timed(lambda: ctx.moe_quant(x, q, sf, T, H, stream=s)), cpu=O and (lambda: O.moe_quant(xh, T, H)))
     sc = torch.empty(1, dtype=torch.float32, device="cuda")
     parts = torch.empty(2048, dtype=torch.float32, device="cuda")
     add("per-tensor fp8 pair (amax+apply)", "kern_quant_fp8_{amax,apply}_v2", f"{T}x{H}",
-        2 * T * H * 2 + T * H, timed(lambda: ctx.quant_fp8_tensor(x, q, sc, parts, T * H, stream=s)))
+        2 * T * H * 2 + T * H, timed(lambda: ctx.quant_fp8_tensor(x, q, sc, parts, T * H, stream=s)),
+        cpu=O and (lambda: O.quant_fp8_apply(xh, T * H, O.quant_fp8_amax(xh, T * H, 2048), 2048)))
+    del xh
     del ro, q, sf
     # config 3: KDA span gather + output gate (24 heads x 128)
     inner = 3072
@@ -199,12 +244,16 @@ def bench_ops(ctx, reps: int, out_path: str | None) -> list:
     at0 = torch.zeros(1, dtype=torch.int32, device="cuda")
     add("KDA span gather (cfg 3a)", "kern_k3_span_gather", f"T={T} 24x128",
         3 * T * inner * 2 * 2 + 3 * 4 * inner * 4 + 2 * 3 * 3 * inner * 2 + T * (24 + 128) * 4 + T * 24 * 2 + T * 128 * 2,
-        timed(lambda: ctx.span_gather(part, cw, state, line, 1628160, wsm, sq, sk, sv, beta, flow, at0, T, stream=s)))
+        timed(lambda: ctx.span_gather(part, cw, state, line, 1628160, wsm, sq, sk, sv, beta, flow, at0, T, stream=s)),
+        cpu=O and (lambda a=(h(part), h(cw), np.zeros((3, 3, inner), np.uint16), h(wsm)):
+                   O.span_gather(a[0], a[1], a[2], a[3], 0, T)))
     attn = bf(T, inner)
     gam = torch.ones(128, dtype=torch.float32, device="cuda")
     gated = torch.empty((T, inner), dtype=torch.bfloat16, device="cuda")
     add("KDA output gate (cfg 3b)", "kern_k3_kda_out_gate", f"T={T} 24x128",
-        3 * T * inner * 2 + 512, timed(lambda: ctx.kda_out_gate(attn, part, gam, gated, at0, T, stream=s)))
+        3 * T * inner * 2 + 512, timed(lambda: ctx.kda_out_gate(attn, part, gam, gated, at0, T, stream=s)),
+        cpu=O and (lambda a=(h(attn), h(part), h(gam), np.zeros((T, inner), np.uint16)):
+                   O.kda_out_gate(a[0], a[1], a[2], a[3], 0, T)))
     del part, sq, sk, sv, attn, gated, wsm
     # config 4: MLA prep (reference form, bf16 partial) and the RoPE + pack form
     mp = bf(T, 5184)
@@ -215,14 +264,18 @@ def bench_ops(ctx, reps: int, out_path: str | None) -> list:
     mg = torch.empty((T, 3072), dtype=torch.bfloat16, device="cuda")
     add("MLA prep (cfg 4, reference form)", "k3h_mla_prep_fused", f"T={T} [T,5184] bf16",
         T * 5184 * 2 + T * (1536 + 576 + 3072) * 2 + 4096,
-        timed(lambda: ctx.mla_prep(mp, gq, gk, slots, slab, 0, qn, mg, T, page_stride=64 * 576, stream=s)))
+        timed(lambda: ctx.mla_prep(mp, gq, gk, slots, slab, 0, qn, mg, T, page_stride=64 * 576, stream=s)),
+        cpu=O and (lambda a=(h(mp), h(gq), h(gk), h(slots), h(slab)):
+                   O.mla_prep(a[0], a[1], a[2], a[3], a[4], 0, 64 * 576, T)))
     del mp, qn, mg
     lat, kr, qq = bf(T, 512), bf(T, 64), bf(T, 16, 192)
     lo = torch.empty((T, 576), dtype=torch.bfloat16, device="cuda")
     qo = torch.empty_like(qq)
     add("MLA latent norm + RoPE + q pack", "k3h_mla_rope_pack", f"T={T} H=16",
         T * (512 + 64 + 16 * 192) * 2 + T * (576 + 16 * 192) * 2,
-        timed(lambda: ctx.mla_rope_pack(lat, kr, qq, gk, slots, lo, qo, T, 16, stream=s)))
+        timed(lambda: ctx.mla_rope_pack(lat, kr, qq, gk, slots, lo, qo, T, 16, stream=s)),
+        cpu=O and (lambda a=(h(lat), h(kr), h(qq), h(gk), h(slots)):
+                   O.mla_rope_pack(a[0], a[1], a[2], a[3], a[4], T, 16)))
     del lat, kr, qq, lo, qo, slab
     # config 5: MoE routing + EP dispatch / finalize (top-8 of 224, EP rank 0 of 4)
     Sx = torch.randn((T, 224), generator=g, device="cuda")
@@ -232,7 +285,8 @@ def bench_ops(ctx, reps: int, out_path: str | None) -> list:
     wts = torch.empty((T, 8), dtype=torch.float32, device="cuda")
     add("router top-8 (cfg 5a)", "k3h_router_topk_rows", f"[{T},224]", T * 224 * 4 + 896 + 2 * T * 8 * 4,
         timed(lambda: ctx.router_topk(Sx, bias, rs, idx, wts, T, topk=8, stream=s)),
-        "latency-bound (sequential picks)")
+        "latency-bound (sequential picks)",
+        cpu=O and (lambda a=(h(Sx), h(bias), int(h(rs)[0])): O.router_topk(a[0], a[1], a[2], T, 8)))
     E, nblk = 56, T // 256
     cap = T * 8 + E * 128
     bc = torch.empty(nblk * E, dtype=torch.int32, device="cuda")
@@ -254,19 +308,22 @@ def bench_ops(ctx, reps: int, out_path: str | None) -> list:
     live = int((e2p >= 0).sum().item())
     add("EP routing tables (count+tables+scatter)", "kern_k3_moe_route_{count,tables,scatter}",
         f"T={T} top-8 E=56", 2 * T * 8 * 4 + 3 * nblk * E * 4 + tpad * 4, t_route,
-        "latency-bound (three launches, one single-workgroup scan)")
+        "latency-bound (three launches, one single-workgroup scan)",
+        cpu=O and (lambda a=h(idx): cpu_route(O, a, T, nblk, E, cap)))
     x8 = torch.randint(0, 256, (T, H), dtype=torch.uint8, device="cuda", generator=g)
     sf8 = torch.randint(0, 256, (T, H // 32), dtype=torch.uint8, device="cuda", generator=g)
     pq = torch.empty((tpad, H), dtype=torch.uint8, device="cuda")
     psf = torch.empty((tpad, H // 32), dtype=torch.uint8, device="cuda")
     add("MXFP8 permute (cfg 5c)", "k3h_moe_permute_mx", f"{tpad} rows x {H}", 2 * tpad * (H + H // 32),
-        timed(lambda: ctx.moe_permute_mx(x8, sf8, rmap, tp, H, pq, psf, stream=s)))
+        timed(lambda: ctx.moe_permute_mx(x8, sf8, rmap, tp, H, pq, psf, stream=s)),
+        cpu=O and (lambda a=(h(x8), h(sf8), h(rmap)): O.moe_permute_mx(a[0], a[1], a[2], tpad, H)))
     del pq, psf, x8, sf8
     fc2 = bf(tpad, H)
     out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
     add("weighted finalize (cfg 5d)", "kern_k3_moe_finalize", f"T={T} cols={H}",
         live * H * 2 + 2 * T * 8 * 4 + T * H * 2,
-        timed(lambda: ctx.moe_finalize(fc2, e2p, wts, out, T, H, topk=8, stream=s)))
+        timed(lambda: ctx.moe_finalize(fc2, e2p, wts, out, T, H, topk=8, stream=s)),
+        cpu=O and (lambda a=(h(fc2), h(e2p), h(wts)): O.moe_finalize(a[0], a[1], a[2], T, 8, H)))
     del fc2, out
     bench_push_land(ctx, add, timed, bf, g, s)
 
@@ -286,6 +343,13 @@ def bench_ops(ctx, reps: int, out_path: str | None) -> list:
         with open(out_path, "w") as f:
             json.dump(rows, f, indent=1)
     return rows
+
+
+def cpu_route(O, ids, T, nblk, E, cap) -> None:
+    """The oracle's count -> tables -> scatter chain for EP rank 0 (CPU baseline)."""
+    bc = O.route_count(ids, T, 8, 0, E)
+    tb = O.route_tables(bc, nblk, E, 128, cap)
+    O.route_scatter(ids, tb["blockoff"], T, 8, 0, E, tb["route_map"])
 
 
 def bench_push_land(ctx, add, timed, bf, g, s) -> None:
@@ -511,6 +575,36 @@ def traffic_table(fetch_csv: str, write_csv: str, ops_json: str) -> str:
     return "\n".join(out)
 
 
+def ops_markdown(ops_json: str) -> str:
+    """Markdown tables of a bench.py --ops-out JSON: the HBM-bound ops (GB/s, % of
+    8 TB/s, % of the run's copy ceiling, CPU oracle column where timed) and the
+    MFMA-bound ops (TFLOP/s, % of the 5.0 PFLOP/s e4m3 peak)."""
+    ops = json.load(open(ops_json))
+    copy = next((r["gbs"] for r in ops if r["kernel"] == "k3h_stream_copy"), None)
+    thr = next((r["cpu_threads"] for r in ops if "cpu_threads" in r), None)
+    out = ["| op | kernel | shape | algorithmic bytes | median us | p10 us | p90 us | GB/s | % of 8 TB/s "
+           f"| % of copy | CPU ms{f' ({thr} threads)' if thr else ''} | CPU GB/s | GPU / CPU | note |",
+           "|---|---|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---|"]
+    for r in ops:
+        if r.get("bound") == "mfma":
+            continue
+        c = (f"{r['cpu_ms']:.1f} | {r['cpu_gbs']:.2f} | {r['gbs'] / r['cpu_gbs']:.0f}x"
+             if "cpu_ms" in r else " | | ")
+        pc = f"{100 * r['gbs'] / copy:.0f}" if copy else ""
+        out.append(f"| {r['op']} | `{r['kernel']}` | {r['shape']} | {r['bytes']:,} | {r['us']:.2f} | "
+                   f"{r['us_p10']:.2f} | {r['us_p90']:.2f} | {r['gbs']:.1f} | {r['pct_peak']:.1f} | {pc} | "
+                   f"{c} | {r['note']} |")
+    mf = [r for r in ops if r.get("bound") == "mfma"]
+    if mf:
+        out += ["", "| op | kernel | shape | FLOPs | bytes | median us | p10 us | p90 us | TFLOP/s "
+                "| % of 5.0 PFLOP/s | note |", "|---|---|---|---:|---:|---:|---:|---:|---:|---:|---|"]
+        for r in mf:
+            out.append(f"| {r['op']} | `{r['kernel']}` | {r['shape']} | {r['flops']:,} | {r['bytes']:,} | "
+                       f"{r['us']:.2f} | {r['us_p10']:.2f} | {r['us_p90']:.2f} | {r['tflops']:.1f} | "
+                       f"{r['pct_peak']:.1f} | {r['note']} |")
+    return "\n".join(out)
+
+
 def load_traffic(kernel: str, workload: str):
     p = os.path.join(REPO, "profiles", "traffic.json")
     try:
@@ -536,12 +630,17 @@ def main() -> int:
                     help="also time every op at its config shape (table on stderr)")
     ap.add_argument("--ops-only", action="store_true", help="only the per-op table")
     ap.add_argument("--ops-out", default=None, help="write the per-op table as JSON")
+    ap.add_argument("--ops-table", metavar="OPS_JSON",
+                    help="print the per-op markdown table of an --ops-out JSON; no GPU")
     ap.add_argument("--traffic-table", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "OPS_JSON"),
                     help="print the per-op HBM byte table from two rocprofv3 --pmc CSVs "
                          "(FETCH_SIZE, WRITE_SIZE runs of --ops-only) and an --ops-out JSON; no GPU")
     a = ap.parse_args()
     if a.traffic_table:
         print(traffic_table(*a.traffic_table))
+        return 0
+    if a.ops_table:
+        print(ops_markdown(a.ops_table))
         return 0
     if a.gpus != 1:
         print(f"bench.py measures one GPU only (asked for {a.gpus}); the op family shards "
@@ -554,7 +653,7 @@ def main() -> int:
     ctx = k3h.Ctx()
     rows = a.rows
     if a.ops_only:
-        bench_ops(ctx, max(5, a.steps), a.ops_out)
+        bench_ops(ctx, max(5, a.steps), a.ops_out, 0.0 if a.no_cpu else 3.0)
         return 0
     copy_gbs = copy_ceiling(ctx, rows, a.steps if a.op == "copy" else 20)
     if a.op == "copy":
@@ -603,7 +702,7 @@ def main() -> int:
             "avg_launch_us": round(ms * 1e3, 2), "copy_ceiling_gbs": round(copy_gbs, 1)}
     ops = None
     if a.ops:
-        ops = bench_ops(ctx, 50, a.ops_out)
+        ops = bench_ops(ctx, 50, a.ops_out, 0.0 if a.no_cpu else 3.0)
     cpu = None
     if not a.no_cpu:
         log("CPU baseline: C oracle on the same inputs")

@@ -48,10 +48,9 @@
 // tiles and scales of a step are brought into LDS by direct-to-LDS loads one
 // step ahead of the MFMAs (two stages; two workgroups per CU).  The epilogues
 // pass the accumulators through LDS so that each lane owns whole output rows
-// (16-byte stores; the fc1 MX blocks quantised in registers).  Consecutive x of
-// a tile land on consecutive XCDs (round-robin dispatch), and with N / 256 a
-// multiple of 8 every tile's column block x stays on XCD x % 8, so each XCD's
-// L2 holds one eighth of every expert's weights.
+// (16-byte stores; the fc1 MX blocks quantised in registers).  The workgroup's
+// linear id picks its item from its XCD's share (k3g_item below), so that each
+// XCD's L2 serves a fixed part of the live tiles and of the column blocks.
 #include "../common/k3_dev.h"
 #include <type_traits>
 
