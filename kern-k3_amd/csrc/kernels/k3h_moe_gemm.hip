@@ -137,8 +137,10 @@ extern "C" __global__ void __launch_bounds__(256) kern_k3h_moe_sf_tile(
 // 7%).  The tile's A scales for the whole of K (128 rows x K/32 bytes) are
 // loaded once, before the first stage, into a table behind the stages
 // (measured: one 4-byte load per row and step, 32 gathered rows per
-// instruction, cost fc1 15%).  The table holds KGM bytes per row: entries for
-// K <= 3584 (KGM 112) keep two workgroups per CU (2 x 78 KB of LDS); the "_w"
+// instruction, cost fc1 15%).  The table holds KGM bytes per row at a row
+// stride of KGM + 4 bytes (an odd number of dwords, so the 32 rows a wave reads
+// hit 32 different banks; at 112 bytes rows r and r + 16 shared one): entries
+// for K <= 3584 (KGM 112) keep two workgroups per CU (2 x 79 KB of LDS); the "_w"
 // entries (KGM 224) take K <= 7168.  Two stages and at most 256 registers per
 // wave let two workgroups share a CU, so one computes while the other waits at
 // its step barrier (measured: 3 stages at one workgroup per CU ran fc1 / fc2 at
@@ -154,32 +156,40 @@ extern "C" __global__ void __launch_bounds__(256) kern_k3h_moe_sf_tile(
 static_assert(K3G_STAGES == 2, "the main loop alternates two stages");
 
 typedef __attribute__((address_space(3))) void k3g_lds_t;
+#define K3G_SAT_ROW(KGM) ((KGM) + 4)  // A-scale table row stride (bytes)
 
 // The workgroup's LDS: the operand stages of the main loop, then the epilogue's
 // transposition tiles (one object shared by every caller in a kernel).
 #define K3G_EP_BYTES (4 * 64 * 272)  // the bf16 epilogue's four 64-row tiles
 template <int KGM>
 K3_DEV uint8_t* k3g_smem() {
-  constexpr int kMain = K3G_SAT_OFF + 128 * KGM;
+  constexpr int kMain = K3G_SAT_OFF + 128 * K3G_SAT_ROW(KGM);
   __shared__ __attribute__((aligned(16))) uint8_t smem[kMain > K3G_EP_BYTES ? kMain : K3G_EP_BYTES];
   return smem;
 }
 
 // A rows in LDS: row r of the tile's step slice (128 bytes = 8 chunks of 16) at
-// slots 8 r + (c ^ (r & 7)), c = chunk.  One load instruction moves 8 whole
-// 128-byte row slices (lane l: row 8 q + l / 8, chunk (l % 8) ^ (l / 8)), and the
-// MFMA operand reads (lanes of 8 consecutive rows, one chunk each) hit 8
-// different bank groups.
-K3_DEV int k3g_aslot(int r, int c) { return 8 * r + (c ^ (r & 7)); }
+// slots 8 r + (c ^ g(r)), c = chunk, g(r) = (r % 8) ^ ((r / 8) % 2).  One load
+// instruction moves 8 whole 128-byte row slices (lane l of instruction q: row
+// 8 q + l / 8, chunk (l % 8) ^ g(row)).  An MFMA operand read takes one chunk of
+// 32 consecutive rows; LDS serves a 16-byte read in groups of 16 lanes over
+// 64 four-byte banks (256 bytes), and 16 consecutive rows r0 .. r0 + 15 (r0 a
+// multiple of 16) land in the 16 distinct 16-byte bank groups
+// 8 (r % 2) + (c ^ g(r)) -- with g(r) = r % 8 alone, rows r and r + 8 shared a
+// bank group (measured: 2-way conflicts on every A operand read).  The same
+// layout is conflict-free for 8-lane groups over 32 banks (g takes 8 values on
+// 8 consecutive rows).
+K3_DEV int k3g_aslot(int r, int c) { return 8 * r + (c ^ ((r & 7) ^ ((r >> 3) & 1))); }
 
 K3_DEV void k3g_issue_stage(uint8_t* st, const uint8_t* a, const uint32_t* arow,
                             const uint8_t* wblk, int ks, int KT, int w, int lane) {
   const int k0 = ks * K3G_KSTEP;
-  const int c = (lane & 7) ^ (lane >> 3);  // the chunk this lane moves (row 8 q + lane / 8)
 #pragma unroll
-  for (int b = 0; b < 4; ++b)  // rows 32 w + 8 b .. + 8 of the tile
+  for (int b = 0; b < 4; ++b) {  // rows 32 w + 8 b .. + 8 of the tile (q = 4 w + b)
+    const int c = (lane & 7) ^ (lane >> 3) ^ (b & 1);  // the chunk this lane moves
     __builtin_amdgcn_global_load_lds(a + arow[b] + k0 + 16 * c,
                                      (k3g_lds_t*)(st + (4 * w + b) * 1024), 16, 0, 0);
+  }
 #pragma unroll
   for (int b = 0; b < 4; ++b) {  // B blocks: tiles 2 w, 2 w + 1, both substeps
     const int T = 2 * w + (b >> 1), s = b & 1;
@@ -224,7 +234,7 @@ K3_DEV void k3g_lds_loop(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
     int src = a_rows ? a_rows[r] : r;
     src = src < 0 ? 0 : src;
     const uint32_t* sr = (const uint32_t*)(a_sf + (size_t)src * KG);
-    uint32_t* dr = (uint32_t*)(sat + row * KGM);
+    uint32_t* dr = (uint32_t*)(sat + row * K3G_SAT_ROW(KGM));
 #pragma unroll 8
     for (int d = d0; d < d1; ++d) dr[d] = sr[d];
   }
@@ -250,7 +260,7 @@ K3_DEV void k3g_lds_loop(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
     return *(const k3_u4*)(st + 16384 + ((4 * wn + nt) * 2 + s) * 1024 + 16 * lane);
   };
   auto rd_sa = [&](int ks, int mt) -> uint32_t {
-    return *(const uint32_t*)(sat + (32 * (2 * wm + mt) + j) * KGM + 4 * ks);
+    return *(const uint32_t*)(sat + (32 * (2 * wm + mt) + j) * K3G_SAT_ROW(KGM) + 4 * ks);
   };
   auto mfma = [&](int mt, int nt, const k3_v8i& av, const k3_u4& bv, uint32_t sa, uint32_t sb,
                   int s) {
