@@ -133,8 +133,13 @@ def cpu_timer(budget_s: float):
 
 def bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0) -> list:
     """Every op at its BASELINE config shape: 5 warm-up launches, then `reps`
-    launches each between two HIP events on the launch stream, with a 512 MB
-    cache-flush write between launches (outside the events); median, p10, p90.
+    launches each between two HIP events on the launch stream, with the caches
+    flushed before each launch (outside the events); median, p10, p90.  Two
+    flushes, each over all reps: "clean" reads a 512 MB buffer (the L2s and the
+    256 MB MALL then hold only clean lines, so the op starts cold and owes no
+    write-back), "dirty" writes a 512 MB buffer (the op then also pays for
+    writing back the dirty lines its own traffic evicts).  The clean figures
+    are the table's; the dirty ones are reported beside them.
     With cpu_budget > 0, the rows of BASELINE configs 1-5 also time the C oracle
     (OpenMP over the host cores) on host copies of the same inputs."""
     import numpy as np
@@ -153,6 +158,7 @@ def bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0) -> 
         return np.ascontiguousarray(t.cpu().numpy())
     s = torch.cuda.current_stream()
     flush = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+    flush_rd = torch.ones(128 << 20, dtype=torch.float32, device="cuda")
     g = torch.Generator(device="cuda")
     g.manual_seed(24301)
 
@@ -162,28 +168,35 @@ def bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0) -> 
     def timed(fn):
         for _ in range(5):
             fn()
-        ts = []
-        for _ in range(reps):
-            flush.fill_(1)
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(s)
-            fn()
-            e1.record(s)
-            e1.synchronize()
-            ts.append(e0.elapsed_time(e1) * 1e3)
-        ts.sort()
-        pick = lambda f: ts[min(len(ts) - 1, int(f * len(ts)))]
-        return pick(0.5), pick(0.1), pick(0.9)
+        out = []
+        for clean in (True, False):
+            ts = []
+            for _ in range(reps):
+                if clean:
+                    flush_rd.sum()
+                else:
+                    flush.fill_(1)
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(s)
+                fn()
+                e1.record(s)
+                e1.synchronize()
+                ts.append(e0.elapsed_time(e1) * 1e3)
+            ts.sort()
+            pick = lambda f: ts[min(len(ts) - 1, int(f * len(ts)))]
+            out += [pick(0.5), pick(0.1), pick(0.9)]
+        return tuple(out)
 
     rows = []
 
     def add(op, kernel, shape, nbytes, t, note="", cpu=None):
-        us, p10, p90 = t
+        us, p10, p90, us_d = t[:4]
         gbs = nbytes / (us * 1e-6) / 1e9
         row = {"op": op, "kernel": kernel, "shape": shape, "bytes": int(nbytes),
-               "launches": 5 + reps,
+               "launches": 5 + 2 * reps,
                "us": round(us, 2), "us_p10": round(p10, 2), "us_p90": round(p90, 2),
                "gbs": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1),
+               "us_dirty": round(us_d, 2), "gbs_dirty": round(nbytes / (us_d * 1e-6) / 1e9, 1),
                "note": note}
         cpu_txt = ""
         if cpu is not None and O is not None:
@@ -193,7 +206,7 @@ def bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0) -> 
             cpu_txt = f" | CPU {sec * 1e3:8.1f} ms {nbytes / sec / 1e9:6.2f} GB/s"
         rows.append(row)
         log(f"{op:42s} {us:8.2f} us (p10 {p10:7.2f}, p90 {p90:7.2f}) {gbs:7.0f} GB/s "
-            f"{100 * gbs / PEAK_GBS:5.1f}%{cpu_txt}  {note}")
+            f"{100 * gbs / PEAK_GBS:5.1f}% | dirty {us_d:8.2f} us{cpu_txt}  {note}")
 
     T = 16384
     # copy ceiling
@@ -328,10 +341,11 @@ def bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0) -> 
     bench_push_land(ctx, add, timed, bf, g, s)
 
     def add_flop(op, kernel, shape, flops, nbytes, t, note=""):
-        us, p10, p90 = t
+        us, p10, p90, us_d = t[:4]
         tf = flops / (us * 1e-6) / 1e12
         rows.append({"op": op, "kernel": kernel, "shape": shape, "bytes": int(nbytes),
-                     "flops": int(flops), "bound": "mfma", "launches": 5 + reps,
+                     "flops": int(flops), "bound": "mfma", "launches": 5 + 2 * reps,
+                     "us_dirty": round(us_d, 2),
                      "us": round(us, 2), "us_p10": round(p10, 2), "us_p90": round(p90, 2),
                      "tflops": round(tf, 1), "pct_peak": round(100 * tf / PEAK_MX_TFLOPS, 1),
                      "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "note": note})
@@ -583,25 +597,28 @@ def ops_markdown(ops_json: str) -> str:
     copy = next((r["gbs"] for r in ops if r["kernel"] == "k3h_stream_copy"), None)
     thr = next((r["cpu_threads"] for r in ops if "cpu_threads" in r), None)
     out = ["| op | kernel | shape | algorithmic bytes | median us | p10 us | p90 us | GB/s | % of 8 TB/s "
-           f"| % of copy | CPU ms{f' ({thr} threads)' if thr else ''} | CPU GB/s | GPU / CPU | note |",
-           "|---|---|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---|"]
+           "| % of copy | us, dirty flush | GB/s, dirty flush "
+           f"| CPU ms{f' ({thr} threads)' if thr else ''} | CPU GB/s | GPU / CPU | note |",
+           "|---|---|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---|"]
     for r in ops:
         if r.get("bound") == "mfma":
             continue
         c = (f"{r['cpu_ms']:.1f} | {r['cpu_gbs']:.2f} | {r['gbs'] / r['cpu_gbs']:.0f}x"
              if "cpu_ms" in r else " | | ")
         pc = f"{100 * r['gbs'] / copy:.0f}" if copy else ""
+        d = f"{r['us_dirty']:.2f} | {r['gbs_dirty']:.1f}" if "us_dirty" in r else " | "
         out.append(f"| {r['op']} | `{r['kernel']}` | {r['shape']} | {r['bytes']:,} | {r['us']:.2f} | "
                    f"{r['us_p10']:.2f} | {r['us_p90']:.2f} | {r['gbs']:.1f} | {r['pct_peak']:.1f} | {pc} | "
-                   f"{c} | {r['note']} |")
+                   f"{d} | {c} | {r['note']} |")
     mf = [r for r in ops if r.get("bound") == "mfma"]
     if mf:
         out += ["", "| op | kernel | shape | FLOPs | bytes | median us | p10 us | p90 us | TFLOP/s "
-                "| % of 5.0 PFLOP/s | note |", "|---|---|---|---:|---:|---:|---:|---:|---:|---:|---|"]
+                "| % of 5.0 PFLOP/s | us, dirty flush | note |",
+                "|---|---|---|---:|---:|---:|---:|---:|---:|---:|---:|---|"]
         for r in mf:
             out.append(f"| {r['op']} | `{r['kernel']}` | {r['shape']} | {r['flops']:,} | {r['bytes']:,} | "
                        f"{r['us']:.2f} | {r['us_p10']:.2f} | {r['us_p90']:.2f} | {r['tflops']:.1f} | "
-                       f"{r['pct_peak']:.1f} | {r['note']} |")
+                       f"{r['pct_peak']:.1f} | {r.get('us_dirty', float('nan')):.2f} | {r['note']} |")
     return "\n".join(out)
 
 
