@@ -20,8 +20,13 @@
 // the deterministic k3_expf.  Both therefore have an exact CPU counterpart.
 //
 // Rows that are read or written once (partial, prefix, prefix2, normed) move
-// with non-temporal loads and stores; gamma, sw and the candidate rows (read
-// in both passes of the mix) stay cacheable.
+// with non-temporal loads and stores; gamma and sw stay cacheable.  Candidate
+// rows: with one or two candidates (held in registers, read once) non-temporal;
+// otherwise pass 1 reads them cacheable, so that pass 2 finds them in L2, and
+// pass 2, their last use, reads them non-temporally (measured at B = 4096:
+// nb 8 164 -> 151 us with a cold cache; cacheable everywhere, the loads also
+// allocate in the MALL and, after a write-heavy predecessor, pay for evicting
+// its dirty lines: nb 2 93 -> 70 us with non-temporal loads).
 #pragma once
 #include "../common/k3_dev.h"
 
@@ -142,7 +147,7 @@ K3_DEV void k3_attnres_mix(const uint16_t* __restrict__ blk_row, k3_u4* pv,
 #pragma unroll
     for (int c = 0; c < NBC; ++c)
 #pragma unroll
-      for (int v = 0; v < K3_KVPT; ++v) xr[c][v] = k3_ld16(blk_row + (size_t)c * K3_H + k3_vec_off(t, v));
+      for (int v = 0; v < K3_KVPT; ++v) xr[c][v] = k3_ld16_nt(blk_row + (size_t)c * K3_H + k3_vec_off(t, v));
   }
   float sq[K3_NB_MAX + 1], dp[K3_NB_MAX + 1], dm[K3_NB_MAX];
 #pragma unroll
@@ -287,7 +292,7 @@ K3_DEV void k3_attnres_mix(const uint16_t* __restrict__ blk_row, k3_u4* pv,
 #pragma unroll
     for (int c = 0; c < K3_NB_MAX; ++c) {
       if (RES || c >= nb) break;
-      xb[slot][c] = k3_ld16(blk_row + (size_t)c * K3_H + u);
+      xb[slot][c] = k3_ld16_nt(blk_row + (size_t)c * K3_H + u);
     }
   };
   // Pass 2 walks the vectors last-read-first: the candidates pass 1 touched last
