@@ -104,7 +104,7 @@ extern "C" __global__ void __launch_bounds__(K3_RES_THREADS) kern_k3_attnres_rms
   if (snapshot && nb < K3_NB_MAX) {
 #pragma unroll
     for (int v = 0; v < K3_KVPT; ++v)
-      k3_st16(blocks + ((size_t)b * K3_NB_MAX + nb) * K3_H + k3_vec_off(t, v), pv[v]);
+      k3_st16_nt(blocks + ((size_t)b * K3_NB_MAX + nb) * K3_H + k3_vec_off(t, v), pv[v]);
   }
   const K3NormedDst dst = {normed_all + dst_off, dst_peer, dst_off, rank, nr};
 #if K3_PUSH >= 2
