@@ -1,0 +1,85 @@
+"""CPU checks of bench.py's measurement tables on synthetic inputs: the rocprofv3
+counter CSV reader, the copy-calibrated HBM byte table and the per-op markdown
+table.  No GPU: the CSVs and the ops JSON are written here."""
+import csv
+import json
+import os
+import sys
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, REPO)
+import bench  # noqa: E402
+
+COPY_BYTES = 1 << 20  # the synthetic copy moves 1 MiB in and 1 MiB out
+
+
+def _pmc_csv(path, counter, per_kernel):
+    """rocprofv3-style counter_collection.csv: one row per dispatch, in the order given."""
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"])
+        w.writeheader()
+        did = 0
+        for name, values in per_kernel:
+            for v in values:
+                did += 1
+                w.writerow({"Dispatch_Id": did, "Kernel_Name": name + "(int, float*)",
+                            "Counter_Name": counter, "Counter_Value": v})
+
+
+def _ops_json(path):
+    rows = [
+        {"op": "stream copy (ceiling)", "kernel": "k3h_stream_copy", "shape": "s", "bytes": 2 * COPY_BYTES,
+         "launches": 3, "us": 2.0, "us_p10": 1.9, "us_p90": 2.1, "gbs": 1048.6, "pct_peak": 13.1,
+         "us_dirty": 2.0, "gbs_dirty": 1048.6, "note": ""},
+        {"op": "residual+RMSNorm+MXFP8 (cfg 2)", "kernel": "k3h_residual_rms_mxfp8", "shape": "s",
+         "bytes": 3 * COPY_BYTES, "launches": 3, "us": 4.0, "us_p10": 3.9, "us_p90": 4.2, "gbs": 786.4,
+         "pct_peak": 9.8, "us_dirty": 5.0, "gbs_dirty": 629.1, "note": "n", "cpu_ms": 2.0,
+         "cpu_gbs": 1.57, "cpu_threads": 16},
+        {"op": "MoE fc2 (MX GEMM, bf16 out)", "kernel": "kern_k3h_moe_gemm_bf16", "shape": "s",
+         "bytes": 10, "flops": 1000, "bound": "mfma", "launches": 3, "us": 1.0, "us_p10": 1.0,
+         "us_p90": 1.0, "tflops": 0.001, "pct_peak": 0.0, "gbs": 0.01, "us_dirty": 1.5, "note": ""},
+    ]
+    json.dump(rows, open(path, "w"))
+    return rows
+
+
+def test_counter_values_keep_dispatch_order_per_kernel(tmp_path):
+    p = tmp_path / "c.csv"
+    _pmc_csv(p, "FETCH_SIZE", [("a", [3.0, 1.0]), ("b", [7.0]), ("a", [2.0])])
+    v = bench.counter_values(str(p), "FETCH_SIZE")
+    assert v == {"a": [3.0, 1.0, 2.0], "b": [7.0]}
+    assert bench.counter_values(str(p), "WRITE_SIZE") == {}
+
+
+def test_traffic_table_calibrates_on_the_copy(tmp_path):
+    # the copy's counters read half (FETCH) and twice (WRITE) its true bytes: the
+    # factors 2 and 0.5 must map the fused kernel's counters onto 2 MiB read + 1 MiB written
+    kib = COPY_BYTES / 1024
+    f, w = tmp_path / "f.csv", tmp_path / "w.csv"
+    _pmc_csv(f, "FETCH_SIZE", [("k3h_stream_copy", [kib / 2] * 3), ("k3h_residual_rms_mxfp8", [kib] * 3)])
+    _pmc_csv(w, "WRITE_SIZE", [("k3h_stream_copy", [kib * 2] * 3),
+                               ("k3h_residual_rms_mxfp8", [kib / 2, kib * 9, kib / 2])])
+    ops = tmp_path / "ops.json"
+    _ops_json(ops)
+    table = bench.traffic_table(str(f), str(w), str(ops))
+    assert "FETCH_SIZE x 2.00000, WRITE_SIZE x 0.50000" in table
+    row = next(l for l in table.splitlines() if l.startswith("| residual+RMSNorm+MXFP8"))
+    cells = [c.strip() for c in row.strip("|").split("|")]
+    # read 2 MiB, written = median of (0.25, 4.5, 0.25) MiB = 0.25 MiB
+    assert cells[2] == f"{2 * COPY_BYTES:,}" and cells[3] == f"{COPY_BYTES // 4:,}"
+    assert cells[-1] == f"{(2 * COPY_BYTES + COPY_BYTES // 4) / (3 * COPY_BYTES):.3f}"
+
+
+def test_ops_markdown_columns(tmp_path):
+    ops = tmp_path / "ops.json"
+    rows = _ops_json(ops)
+    md = bench.ops_markdown(str(ops)).splitlines()
+    hbm = [l for l in md if l.startswith("| residual+RMSNorm+MXFP8")]
+    assert len(hbm) == 1
+    cells = [c.strip() for c in hbm[0].strip("|").split("|")]
+    assert cells[9] == f"{100 * rows[1]['gbs'] / rows[0]['gbs']:.0f}"  # % of the copy row
+    assert cells[10] == "5.00" and cells[11] == "629.1"                  # dirty-flush time and rate
+    assert cells[12] == "2.0" and cells[13] == "1.57"                    # CPU oracle columns
+    assert cells[14] == f"{rows[1]['gbs'] / rows[1]['cpu_gbs']:.0f}x"
+    assert any(l.startswith("| MoE fc2") for l in md)                    # MFMA table
+    assert not any(l.startswith("| MoE fc2") and "629" in l for l in md)
