@@ -57,6 +57,28 @@ def test_router_topk(ctx, T, topk):
     _eq("wts", wts.view(np.uint32), want_w.view(np.uint32))
 
 
+@pytest.mark.parametrize("topk", [8, 16])
+def test_router_topk_ties(ctx, topk):
+    """Equal keys: rows of one repeated logit (every key equal), rows whose logits
+    repeat with period 32 or 64 (equal keys in different slots of one lane and in
+    different lanes), and odd row counts; ties must go to the smallest expert id."""
+    _case(f"router_topk ties topk={topk}")
+    T = 9
+    S = np.zeros((T, 224), np.float32)
+    S[1] = 0.5
+    S[2] = np.tile(np.linspace(-1, 1, 32, dtype=np.float32), 7)
+    S[3] = np.tile(np.linspace(1, -1, 64, dtype=np.float32), 4)[:224]
+    S[4] = np.repeat(np.float32([0.25, -0.25, 1.0, 0.0, 2.0, -2.0, 0.75]), 32)
+    S[5:] = np.random.default_rng(77).integers(-2, 3, (T - 5, 224)).astype(np.float32)
+    bias = np.zeros(224, np.float32)
+    rs = np.array([0x4020], np.uint16)  # bf16 2.5
+    want_i, want_w = O.router_topk(S, bias, rs[0], T, topk)
+    assert (want_i[0] == np.arange(topk)).all()  # all keys equal: experts 0 .. topk - 1
+    idx, wts = _run_router(ctx, S, bias, rs, T, topk)
+    _eq("idx", idx, want_i)
+    _eq("wts", wts.view(np.uint32), want_w.view(np.uint32))
+
+
 def test_argmax_f32(ctx):
     _case("argmax")
     g = rng(1400)
