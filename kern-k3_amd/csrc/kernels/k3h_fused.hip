@@ -19,9 +19,9 @@
 // two rows, one per 128-thread half; within a half, thread t owns the 16-byte
 // vectors t + 128 v of its row (the K1 ownership, so the sum of squares has the
 // K1 order), and a 32-value MX block is the vectors of four consecutive lanes
-// at the same v.  Measured back to back at 16384 rows: one, two and
-// four rows per workgroup 134.8, 134.5 and 137.4 us.  The E8M0 bytes of four quads are gathered into one lane and
-// stored as a word, after the quantisation loop.  A half whose row is past B
+// at the same v.  Measured back to back at 16384 rows: one, two and four rows
+// per workgroup 134.8, 134.5 and 137.4 us.  The E8M0 bytes of four quads are
+// gathered into one lane and stored as a word, after the quantisation loop.  A half whose row is past B
 // still takes part in the workgroup barrier but stores nothing.
 //
 // Wait discipline: the vector memory counter counts stores as well as loads,
