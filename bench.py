@@ -338,7 +338,7 @@ def bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0) -> 
         timed(lambda: ctx.moe_finalize(fc2, e2p, wts, out, T, H, topk=8, stream=s)),
         cpu=O and (lambda a=(h(fc2), h(e2p), h(wts)): O.moe_finalize(a[0], a[1], a[2], T, 8, H)))
     del fc2, out
-    bench_push_land(ctx, add, timed, bf, g, s)
+    bench_push_land(ctx, add, timed, bf, g, s, O, h)
 
     def add_flop(op, kernel, shape, flops, nbytes, t, note=""):
         us, p10, p90, us_d = t[:4]
@@ -366,11 +366,13 @@ def cpu_route(O, ids, T, nblk, E, cap) -> None:
     O.route_scatter(ids, tb["blockoff"], T, 8, 0, E, tb["route_map"])
 
 
-def bench_push_land(ctx, add, timed, bf, g, s) -> None:
+def bench_push_land(ctx, add, timed, bf, g, s, O=None, h=None) -> None:
     """The residual push family and the landing kernels at one TP rank's share of
     the 16k prefill (B = tokens / 4 = 4096 rows; manifest shapes).  On one GPU
     the four ranks' normed_all buffers are local, so every normed copy is an HBM
-    write here (three of the four cross xGMI on a 4-GPU node)."""
+    write here (three of the four cross xGMI on a 4-GPU node).  With the oracle
+    module O (and the host-copy helper h) the single-rank rows also time the C
+    oracle; the push rows have no CPU counterpart of their multi-rank stores."""
     import torch
     B, HH = 4096, H
     row = B * HH * 2
@@ -398,23 +400,29 @@ def bench_push_land(ctx, add, timed, bf, g, s) -> None:
     add("K1b nb 1 entry (manifest res_mlp)", "kern_k3_land_add_attnres_rms_nb1", f"B={B} nb=1",
         2 * row + row + HH * 4 + HH * 2 + 2 * row,
         timed(lambda: ctx.land_add_attnres_rms_nb(part, prefix, blocks, sw, gm, pre2, nrm, 1, 0, B,
-                                                  stream=s)))
+                                                  stream=s)),
+        cpu=O and (lambda a=(h(part), h(prefix), h(blocks), h(sw), h(gm)):
+                   O.land_add_attnres_rms(a[0], a[1], a[2], a[3], a[4], 1, 0, B)))
     add("res_mlp nb 5 with res_in statistics (nb_stats 4)", "kern_k3_land_add_attnres_rms_nb5",
         f"B={B} nb=5", 2 * row + 5 * row + HH * 4 + HH * 2 + 2 * row + B * 4 * 8,
         timed(lambda: ctx.land_add_attnres_rms_nb_stats(part, prefix, blocks, sw_mlp, gm, pre2, nrm,
-                                                        5, 0, B, stats, 4, stream=s)))
+                                                        5, 0, B, stats, 4, stream=s)),
+        cpu=O and (lambda a=(h(part), h(prefix), h(blocks), h(sw_mlp), h(gm), h(stats)):
+                   O.land_add_attnres_rms_stats(a[0], a[1], a[2], a[3], a[4], 5, 0, B, a[5], 4)))
     del normed, peer, p1, p2, prefix2, hidden, part, pre2, nrm, blocks, prefix
     # landing kernels (k3_land / k3_situ_bf16 / k3_land_fused)
-    h = 3584
-    lat = bf(B, h)
-    gl = bf(h, mean=1.0, std=0.1)
+    hd = 3584
+    lat = bf(B, hd)
+    gl = bf(hd, mean=1.0, std=0.1)
     ln = torch.empty_like(lat)
-    add("rms (l0, h 3584)", "kern_k3_rms", f"B={B} h={h}", 2 * B * h * 2 + h * 2,
-        timed(lambda: ctx.rms(lat, gl, ln, h, B, stream=s)))
-    pf = torch.randn((B, h), generator=g, device="cuda")
-    lo = torch.empty((B, h), dtype=torch.bfloat16, device="cuda")
-    add("land (l0, n 3584)", "kern_k3_land", f"B={B} n={h}", B * h * 4 + B * h * 2,
-        timed(lambda: ctx.land(pf, lo, h, 0, h, B, stream=s)))
+    add("rms (l0, h 3584)", "kern_k3_rms", f"B={B} h={hd}", 2 * B * hd * 2 + hd * 2,
+        timed(lambda: ctx.rms(lat, gl, ln, hd, B, stream=s)),
+        cpu=O and (lambda a=(h(lat), h(gl)): O.rms(a[0], a[1], hd, B)))
+    pf = torch.randn((B, hd), generator=g, device="cuda")
+    lo = torch.empty((B, hd), dtype=torch.bfloat16, device="cuda")
+    add("land (l0, n 3584)", "kern_k3_land", f"B={B} n={hd}", B * hd * 4 + B * hd * 2,
+        timed(lambda: ctx.land(pf, lo, hd, 0, hd, B, stream=s)),
+        cpu=O and (lambda a=h(pf): O.land(a, hd, 0, hd, B)))
     del pf, lo
     for n, kind in ((33792, "f32"), (6144, "f32"), (33792, "situ_bf16")):
         if kind == "f32":
@@ -426,14 +434,16 @@ def bench_push_land(ctx, add, timed, bf, g, s) -> None:
         act = torch.empty((B, n), dtype=torch.bfloat16, device="cuda")
         add(nm, ker, f"B={B} n={n}", B * 2 * n * ib + B * n * 2,
             timed(lambda: ctx.land_situ(p, act, n, B, variant="situ_bf16" if kind != "f32" else None,
-                                        stream=s)))
+                                        stream=s)),
+            cpu=O and (lambda a=h(p): O.land_situ(a, n, B)))
         del p, act
     n = 6144
     sp = bf(B, 2 * n, std=2.0)
     act = torch.empty((B, n), dtype=torch.bfloat16, device="cuda")
-    add("SiTU landing + latent rms (fused)", "kern_k3_situ_rms_bf16", f"B=L={B} n={n} h={h}",
-        B * 2 * n * 2 + B * n * 2 + 2 * B * h * 2 + h * 2,
-        timed(lambda: ctx.situ_rms(sp, act, lat, gl, ln, n, B, h, B, 4 * B, stream=s)))
+    add("SiTU landing + latent rms (fused)", "kern_k3_situ_rms_bf16", f"B=L={B} n={n} h={hd}",
+        B * 2 * n * 2 + B * n * 2 + 2 * B * hd * 2 + hd * 2,
+        timed(lambda: ctx.situ_rms(sp, act, lat, gl, ln, n, B, hd, B, 4 * B, stream=s)),
+        cpu=O and (lambda a=(h(sp), h(lat), h(gl)): O.situ_rms(a[0], a[1], a[2], n, B, hd, B, 4 * B)))
 
 
 def bench_gemm(ctx, add_flop, timed, g, s, rmap, cta_batch, num_tiles, tpad, T, E) -> None:
