@@ -252,10 +252,14 @@ K3H_API int k3h_span_gather(k3h_ctx_t ctx, void* stream, const void* partial, co
                             void* span_beta, void* span_flow, const int* span_at, int span);
 /* kern_k3_kda_out_gate (k3_kda_out_gate_v3.cu:36; op kda_out_gate_v2,
  * json:406169): attn bf16 [span, 3072], gate band 3 of gate_partial bf16
- * [rows, 12288], gamma_o f32 [128] -> gated bf16 rows [at, at + span). */
+ * [rows, 12288], gamma_o f32 [128] -> gated bf16 rows [at, at + span).
+ * eps is the per-head RMSNorm eps, compiled into the module as the reference's
+ * define (k3_kda_out_gate_v3.cu:25): 1e-5f (k3_kda_out_gate_v3+HEADS=24) or
+ * 1e-6f (k3_kda_out_gate_v3+HEADS=24+K11_RMS_EPS=1e-6f); anything else is
+ * K3H_EINVAL. */
 K3H_API int k3h_kda_out_gate(k3h_ctx_t ctx, void* stream, const void* attn,
                              const void* gate_partial, const float* gamma_o, void* gated,
-                             const int* span_at, int span);
+                             const int* span_at, int span, float eps);
 
 /* ---- MLA --------------------------------------------------------------------
  * kern_k3_mla_prep_head + kern_k3_mla_prep_gate (k3_mla_prep_v2.cu:91,130;
@@ -308,7 +312,10 @@ K3H_API int k3h_mla_rope_pack(k3h_ctx_t ctx, void* stream, const void* latent,
  * columns, so that its L2 holds the operands its workgroups share); the grid
  * (N/256, rows) has enough rows for every XCD's share.  N % 256 == 0,
  * K % 128 == 0, K <= 7168; rows of padding tiles route token 0 and are
- * computed.  a_rows values (when given) must index rows of a / a_sf. */
+ * computed.  a_rows values (when given) must index rows of a / a_sf.  Row
+ * offsets into a are 32-bit: without a_rows, max_tiles * 128 * K must not
+ * exceed 2^32 - 1 (else K3H_EINVAL); with a_rows, the caller keeps
+ * token_count * K below 2^32 (the values are on the device, not checked). */
 #define K3H_GEMM_F32 0
 #define K3H_GEMM_BF16 1
 #define K3H_GEMM_SITU_MX 2

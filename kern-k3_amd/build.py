@@ -92,6 +92,7 @@ MODULES = [
     "k3_router_argmax+TOPK=8",
     "k3_span_gather_v3+HEADS=24",
     "k3_kda_out_gate_v3+HEADS=24",
+    "k3_kda_out_gate_v3+HEADS=24+K11_RMS_EPS=1e-6f",
     "k3_mla_prep_v2+INNER=3072+MLA_FUSED=5184",
     "k3_mla_prep_bf16+INNER=3072+MLA_FUSED=5184",
     "k3h_mla_rope",
@@ -111,6 +112,8 @@ DEVICE_FLAGS = [
 ]
 
 HOST_SOURCES = ["k3h_module.cpp", "k3h_ops_residual.cpp", "k3h_ops_push.cpp", "k3h_ops_land.cpp", "k3h_ops_gemm.cpp", "k3h_ops_quant.cpp", "k3h_ops_moe.cpp", "k3h_ops_kda.cpp", "k3h_ops_mla.cpp"]
+# host sources that carry device data (compiled as HIP for gfx950 into the library)
+HOST_HIP_SOURCES: list[str] = []
 
 
 def module_defines(key: str) -> tuple[str, list[str]]:
@@ -149,9 +152,11 @@ def build_host() -> str:
     dst = os.path.join(OUT, "libk3h.so")
     tmp = dst + ".tmp"
     srcs = [os.path.join(CSRC, "host", s) for s in HOST_SOURCES]
+    hip_srcs = [os.path.join(CSRC, "host", s) for s in HOST_HIP_SOURCES]
     cmd = [HIPCC, "-O2", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden",
+           f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
            "-Wall", "-Wextra", "-I", os.path.join(REPO, "include"), "-I", os.path.join(CSRC, "host"),
-           "-o", tmp, *srcs]
+           "-o", tmp, *srcs, *hip_srcs]
     _run(cmd, "libk3h.so")
     os.replace(tmp, dst)
     return dst

@@ -89,6 +89,9 @@ K3H_API int k3h_moe_gemm_mx(k3h_ctx_t ctx, void* stream, int epilogue, const voi
                             int N, int K, void* out, void* out_sf, const float* alpha,
                             const float* beta) {
   if (!ctx || !gemm_shape_ok(E, N, K, max_tiles)) return K3H_EINVAL;
+  // Activation row offsets are 32-bit in the kernels: read in place, every padded
+  // row of every tile must sit below 4 GiB.
+  if (a_rows == nullptr && (int64_t)max_tiles * 128 * K > (int64_t)UINT32_MAX) return K3H_EINVAL;
   if (!gemm_ptrs_ok(a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch)) return K3H_EINVAL;
   K3hArgs args = gemm_args(a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch, E, N, K, max_tiles);
   const bool wide = K > kMaxKNarrow;

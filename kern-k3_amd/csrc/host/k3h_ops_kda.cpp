@@ -30,7 +30,12 @@ K3H_API int k3h_span_gather(k3h_ctx_t ctx, void* stream, const void* partial, co
 
 K3H_API int k3h_kda_out_gate(k3h_ctx_t ctx, void* stream, const void* attn,
                              const void* gate_partial, const float* gamma_o, void* gated,
-                             const int* span_at, int span) {
+                             const int* span_at, int span, float eps) {
+  // eps selects the module: the norm's eps is compiled in (k3_kda_out_gate_v3.cu:25).
+  const char* key;
+  if (eps == 1e-5f) key = "k3_kda_out_gate_v3+HEADS=24";
+  else if (eps == 1e-6f) key = "k3_kda_out_gate_v3+HEADS=24+K11_RMS_EPS=1e-6f";
+  else return K3H_EINVAL;
   if (!ctx || span < 0) return K3H_EINVAL;
   if (span == 0) return K3H_OK;
   if (!k3h_okp(attn, 16) || !k3h_okp(gate_partial, 16) || !k3h_okp(gamma_o, 16) ||
@@ -38,7 +43,7 @@ K3H_API int k3h_kda_out_gate(k3h_ctx_t ctx, void* stream, const void* attn,
     return K3H_EINVAL;
   K3hArgs a;
   a.ptr(attn).ptr(gate_partial).ptr(gamma_o).ptr(gated).ptr(span_at).i32(span);
-  return k3h_run(ctx, "k3_kda_out_gate_v3+HEADS=24", "kern_k3_kda_out_gate", (uint32_t)span,
+  return k3h_run(ctx, key, "kern_k3_kda_out_gate", (uint32_t)span,
                  kHeads / 8, 1, 128, stream, a);
 }
 

@@ -1,4 +1,4 @@
-// Module k3_kda_out_gate_v3+HEADS=24: the KDA output gate (K11).
+// Module k3_kda_out_gate_v3+HEADS=24[+K11_RMS_EPS=1e-6f]: the KDA output gate (K11).
 //
 //   kern_k3_kda_out_gate(attn, gate_partial, gamma_o, gated, span_at, span)
 //       grid (span, HEADS / 8, 1)   block (128, 1, 1)
@@ -6,7 +6,7 @@
 // Entry, parameters and geometry are the reference's (k3_kda_out_gate_v3.cu:36;
 // contract k3_kda_out_gate_v2.cu:5-23; manifest op kda_out_gate_v2,
 // k3-tp4-prefill-16k.json:406169).  For span row i, head h, dv < 128, b = at + i:
-//   a  = f32(attn[i, h*128 + dv]);   r = rsqrt(sum_dv a^2 / 128 + 1e-5)
+//   a  = f32(attn[i, h*128 + dv]);   r = rsqrt(sum_dv a^2 / 128 + eps)
 //   o  = bf16(a * r * gamma_o[dv]);  gt = bf16(sigmoid(g)), g = gate_partial[b, 3*INNER + h*128 + dv]
 //   gated[b, h*128 + dv] = bf16(f32(o) * f32(gt))
 // Thread layout of the reference: 8 heads per workgroup, 16 lanes per head, 8
@@ -23,7 +23,11 @@
 #endif
 #define K11_INNER (HEADS * 128)
 #define K11_KDA_FUSED (4 * K11_INNER)
+// The norm's eps is a compile-time define, as in the reference
+// (k3_kda_out_gate_v3.cu:25): 1e-5 by default, 1e-6 in the +K11_RMS_EPS=1e-6f build.
+#ifndef K11_RMS_EPS
 #define K11_RMS_EPS 1e-5f
+#endif
 static_assert(HEADS % 8 == 0, "HEADS must be a multiple of 8");
 
 // One (row, 16-byte column vector) of the gate: the per-head sum of squares

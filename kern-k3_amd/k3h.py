@@ -79,7 +79,7 @@ _SIGS: dict[str, list] = {
     "k3h_moe_w_shuffle": [_P, _P, _P, _P, _I, _I, _I, _I],
     "k3h_moe_sf_shuffle": [_P, _P, _P, _P, _I, _I, _I, _I],
     "k3h_span_gather": [_P, _P, _P, _P, _P, _P, ctypes.c_int64, _P, _P, _P, _P, _P, _P, _P, _I],
-    "k3h_kda_out_gate": [_P, _P, _P, _P, _P, _P, _P, _I],
+    "k3h_kda_out_gate": [_P, _P, _P, _P, _P, _P, _P, _I, _F],
     "k3h_mla_prep": [_P, _P, _I, _P, _P, _P, _P, _P, ctypes.c_int64, ctypes.c_int64, _P, _P, _I],
     "k3h_mla_rope_pack": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _F, _I, _I],
     "k3h_attnres_rms_push": [_P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I],
@@ -451,11 +451,23 @@ class Ctx:
                                           _ptr(blockcount)), "moe_route_count")
 
     def moe_route_tables(self, blockcount, blocks: int, E: int, tile: int, blockoff, cta_batch,
-                         cta_limit, num_non_exiting, total_padded, route_map, stream=None) -> None:
-        for nm, t in (("blockcount", blockcount), ("blockoff", blockoff), ("cta_batch", cta_batch),
-                      ("cta_limit", cta_limit), ("num_non_exiting", num_non_exiting),
-                      ("total_padded", total_padded), ("route_map", route_map)):
-            _dev(t, nm, I32, 1, align=4)
+                         cta_limit, num_non_exiting, total_padded, route_map, stream=None,
+                         T: int | None = None, topk: int = 16) -> None:
+        """Tables of the counting sort over `blocks` 256-token blocks.  The route
+        tiles number at most (T*topk + (tile-1)*E) // tile (every expert's last
+        tile may be partial), which sizes cta_batch / cta_limit and route_map
+        (T defaults to blocks*256)."""
+        T = blocks * 256 if T is None else T
+        if T > blocks * 256:
+            raise ValueError("moe_route_tables: T exceeds blocks * 256")
+        max_tiles = (T * topk + (tile - 1) * E) // tile
+        _dev(blockcount, "blockcount", I32, blocks * E, align=4)
+        _dev(blockoff, "blockoff", I32, blocks * E, align=4)
+        _dev(cta_batch, "cta_batch", I32, max_tiles, align=4)
+        _dev(cta_limit, "cta_limit", I32, max_tiles, align=4)
+        _dev(num_non_exiting, "num_non_exiting", I32, 1, align=4)
+        _dev(total_padded, "total_padded", I32, 1, align=4)
+        _dev(route_map, "route_map", I32, max_tiles * tile, align=4)
         _check(self.L.k3h_moe_route_tables(self.h, _stream(stream), _ptr(blockcount), blocks, E, tile,
                                            _ptr(blockoff), _ptr(cta_batch), _ptr(cta_limit),
                                            _ptr(num_non_exiting), _ptr(total_padded),
@@ -481,12 +493,17 @@ class Ctx:
                                        _ptr(wts), _ptr(out), T, cols), "moe_finalize")
 
     def moe_permute_mx(self, q, sf, route_map, total_padded, cols: int, pq, psf,
-                       stream=None) -> None:
+                       stream=None, tokens: int | None = None) -> None:
         """pq[r] = q[route_map[r]], psf[r] = sf[route_map[r]] for r < total_padded[0]
-        (a device value), at most the rows pq / psf hold."""
+        (a device value), at most the rows pq / psf hold.  route_map entries index
+        rows of q / sf: with `tokens` given, q and sf must hold that many rows (the
+        entries are device values, so the host checks the capacity it is told)."""
+        if cols <= 0 or cols % 32:
+            raise ValueError("moe_permute_mx: cols must be a positive multiple of 32")
         max_rows = min(pq.numel() // cols, psf.numel() // (cols // 32), route_map.numel())
-        _dev(q, "q", U8, cols)
-        _dev(sf, "sf", U8, cols // 32, align=4)
+        rows_in = 1 if tokens is None else tokens
+        _dev(q, "q", U8, rows_in * cols)
+        _dev(sf, "sf", U8, rows_in * (cols // 32), align=4)
         _dev(route_map, "route_map", I32, 1, align=4)
         _dev(total_padded, "total_padded", I32, 1, align=4)
         _dev(pq, "pq", U8, 1)
@@ -530,15 +547,16 @@ class Ctx:
                                       _ptr(span_at), span), "span_gather")
 
     def kda_out_gate(self, attn, gate_partial, gamma_o, gated, span_at, span: int,
-                     stream=None) -> None:
-        """Manifest op kda_out_gate_v2 -- kern_k3_kda_out_gate, HEADS = 24."""
+                     stream=None, eps: float = 1e-5) -> None:
+        """Manifest op kda_out_gate_v2 -- kern_k3_kda_out_gate, HEADS = 24; eps picks the
+        module (1e-5, or 1e-6 for the +K11_RMS_EPS=1e-6f build)."""
         _dev(attn, "attn", BF16, span * 3072)
         _dev(gate_partial, "gate_partial", BF16, 4 * 3072)
         _dev(gamma_o, "gamma_o", F32, 128)
         _dev(gated, "gated", BF16, 3072)
         _dev(span_at, "span_at", I32, 1, align=4)
         _check(self.L.k3h_kda_out_gate(self.h, _stream(stream), _ptr(attn), _ptr(gate_partial),
-                                       _ptr(gamma_o), _ptr(gated), _ptr(span_at), span),
+                                       _ptr(gamma_o), _ptr(gated), _ptr(span_at), span, eps),
                "kda_out_gate")
 
     # ------------------------------------------------------------ MLA
@@ -595,9 +613,15 @@ class Ctx:
                     beta=None, stream=None) -> None:
         """MX GEMM over the route tiles (epilogue GEMM_F32 / GEMM_BF16 / GEMM_SITU_MX)."""
         rows = max_tiles * 128
-        _dev(a, "a", U8, K, align=16)
-        _dev(a_sf, "a_sf", U8, K // 32, align=4)
-        if a_rows is not None:
+        if a_rows is None:
+            # A is read in place: one row per padded row of every tile (32-bit row offsets)
+            if rows * K > 0xFFFFFFFF:
+                raise ValueError("moe_gemm_mx: max_tiles * 128 * K must stay below 2^32")
+            _dev(a, "a", U8, rows * K, align=16)
+            _dev(a_sf, "a_sf", U8, rows * K // 32, align=4)
+        else:
+            _dev(a, "a", U8, K, align=16)
+            _dev(a_sf, "a_sf", U8, K // 32, align=4)
             _dev(a_rows, "a_rows", I32, rows, align=4)
         _dev(wt, "wt", U8, E * N * K // 2)
         _dev(wsf, "wsf", U8, E * N * K // 32, align=8)

@@ -107,7 +107,7 @@ void k3o_span_gather(const uint16_t* partial, const float* cw, uint16_t* win, co
                      uint16_t* span_q, uint16_t* span_k, uint16_t* span_v, uint16_t* span_beta,
                      uint16_t* span_flow, int at, int span, int heads);
 void k3o_kda_out_gate(const uint16_t* attn, const uint16_t* gate_partial, const float* gamma_o,
-                      uint16_t* gated, int at, int span, int heads);
+                      uint16_t* gated, int at, int span, int heads, float eps);
 
 /* ---- MLA (k3_mla_prep_v2.cu / k3_mla_prep_bf16.cu; RoPE + pack) -------------- */
 void k3o_mla_prep(const float* partial_f32, const uint16_t* partial_bf16, int mla_fused,

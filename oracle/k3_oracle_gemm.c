@@ -79,6 +79,7 @@ void k3o_moe_gemm_mx_abs(const uint8_t* a, const uint8_t* a_sf, const int* a_row
     int used = 0;
     for (int t = 0; t < num_tiles; ++t) used |= cta_batch[t] == e;
     if (!used) continue;
+#pragma omp parallel for schedule(static)
     for (int n = 0; n < N; ++n)
       for (int k = 0; k < K; ++k) {
         const uint8_t* wr = w + ((size_t)e * N + n) * (K / 2);

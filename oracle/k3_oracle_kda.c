@@ -51,11 +51,12 @@ void k3o_span_gather(const uint16_t* partial, const float* cw, uint16_t* win, co
 
 /* kern_k3_kda_out_gate (k3_kda_out_gate_v3.cu:36-118): per (row, head) the sum
  * of squares in the reference order -- 16 lanes with 8 serial fmas each, then
- * a xor butterfly 8, 4, 2, 1 -- r = 1 / sqrt(ss / 128 + 1e-5) (rsqrtf replaced by
- * the correctly rounded form), o = bf16(a r gamma_o), gt = bf16(sigmoid(g)),
+ * a xor butterfly 8, 4, 2, 1 -- r = 1 / sqrt(ss / 128 + eps) (rsqrtf replaced by
+ * the correctly rounded form; eps is the module's K11_RMS_EPS, 1e-5 or 1e-6,
+ * k3_kda_out_gate_v3.cu:25,92), o = bf16(a r gamma_o), gt = bf16(sigmoid(g)),
  * gated = bf16(o gt).  Rows [at, at + span) of gated are written. */
 void k3o_kda_out_gate(const uint16_t* attn, const uint16_t* gate_partial, const float* gamma_o,
-                      uint16_t* gated, int at, int span, int heads) {
+                      uint16_t* gated, int at, int span, int heads, float eps) {
   const int inner = heads * 128, fused = 4 * inner;
 #pragma omp parallel for schedule(static)
   for (int i = 0; i < span; ++i) {
@@ -74,7 +75,7 @@ void k3o_kda_out_gate(const uint16_t* attn, const uint16_t* gate_partial, const 
         for (int l = 0; l < 16; ++l) tmp[l] = lane[l] + lane[l ^ o];
         memcpy(lane, tmp, sizeof(lane));
       }
-      const float r = 1.0f / sqrtf(fmaf(lane[0], 1.0f / 128.0f, 1e-5f));
+      const float r = 1.0f / sqrtf(fmaf(lane[0], 1.0f / 128.0f, eps));
       for (int dv = 0; dv < 128; ++dv) {
         const float a = k3o_bf2f(attn[(size_t)i * inner + h * 128 + dv]);
         const float o = land(a * r * gamma_o[dv]);

@@ -294,10 +294,12 @@ def span_gather(partial, cw, win, wsm, at, span, heads=24):
     return q, k, v, beta, flow, w
 
 
-def kda_out_gate(attn, gate_partial, gamma_o, gated_in, at, span, heads=24):
+def kda_out_gate(attn, gate_partial, gamma_o, gated_in, at, span, heads=24, eps=1e-5):
+    """eps is the module's K11_RMS_EPS (1e-5, or 1e-6 for config 3)."""
     gated = np.ascontiguousarray(gated_in, np.uint16).copy()
     lib().k3o_kda_out_gate(_p(np.ascontiguousarray(attn)), _p(np.ascontiguousarray(gate_partial)),
-                           _p(np.ascontiguousarray(gamma_o, np.float32)), _p(gated), at, span, heads)
+                           _p(np.ascontiguousarray(gamma_o, np.float32)), _p(gated), at, span, heads,
+                           ctypes.c_float(eps))
     return gated
 
 

@@ -111,3 +111,64 @@ def test_grid_expressions():
     assert k3h._eval_expr({"ceil_div": [{"add": ["tokens", 3]}, 2]}, {"tokens": 5}) == 4
     with pytest.raises(ValueError):
         k3h._eval_expr({"pow": [2, 3]}, env)
+
+
+def test_gemm_rejects_32bit_row_offset_overflow(hctx):
+    """A read in place: max_tiles * 128 * K above 2^32 - 1 is rejected before any launch."""
+    L, h = hctx
+    # 4682 tiles * 128 rows * 7168 bytes = 4,295,819,264 > 4,294,967,295
+    assert L.k3h_moe_gemm_mx(h, None, 0, A, A, None, A, A, A, A, 4682, 1, 256, 7168, A,
+                             None, None, None) == k3h.K3H_EINVAL
+
+
+def test_out_gate_eps_selects_module(hctx):
+    L, h = hctx
+    assert L.k3h_kda_out_gate(h, None, A, A, A, A, A, 1, 1e-4) == k3h.K3H_EINVAL
+    assert L.k3h_kda_out_gate(h, None, A, A, A, A, A, 0, 1e-6) == 0   # span 0: no launch
+    assert L.k3h_kda_out_gate(h, None, A, A, A, A, A, 0, 1e-5) == 0
+
+
+def test_wrappers_reject_undersized_buffers(monkeypatch):
+    """The Python mirror checks each buffer against the size the kernel will touch.
+    Without a GPU the tensor check is narrowed to its size part (the device and
+    alignment parts are what host tensors would fail first); every case here is
+    rejected before any call into the library."""
+    import torch
+
+    def size_only(t, name, dtypes, numel=None, align=16):
+        if numel is not None and t.numel() < numel:
+            raise ValueError(f"{name}: needs at least {numel} elements, has {t.numel()}")
+    monkeypatch.setattr(k3h, "_dev", size_only)
+    ctx = k3h.Ctx()
+    i32 = lambda n: torch.zeros(n, dtype=torch.int32)
+    u8 = lambda n: torch.zeros(n, dtype=torch.uint8)
+    blocks, E, T, topk = 4, 56, 1024, 8
+    tiles = (T * topk + 127 * E) // 128
+    good = dict(blockcount=i32(blocks * E), blockoff=i32(blocks * E), cta_batch=i32(tiles),
+                cta_limit=i32(tiles), num_non_exiting=i32(1), total_padded=i32(1),
+                route_map=i32(tiles * 128))
+    for name, small in (("blockcount", i32(1)), ("blockoff", i32(blocks * E - 1)),
+                        ("cta_batch", i32(tiles - 1)), ("route_map", i32(tiles * 128 - 1))):
+        args = dict(good, **{name: small})
+        with pytest.raises(ValueError, match=f"{name}: needs at least"):
+            ctx.moe_route_tables(args["blockcount"], blocks, E, 128, args["blockoff"],
+                                 args["cta_batch"], args["cta_limit"], args["num_non_exiting"],
+                                 args["total_padded"], args["route_map"], T=T, topk=topk)
+    # GEMM reading A in place needs every padded row of max_tiles tiles
+    K, N, mt = 256, 256, 3
+    with pytest.raises(ValueError, match="a: needs at least"):
+        ctx.moe_gemm_mx(ctx.GEMM_F32, u8(mt * 128 * K - 16), u8(mt * 128 * K // 32), None,
+                        u8(E * N * K // 2), u8(E * N * K // 32), i32(1), i32(mt), mt, E, N, K,
+                        torch.zeros(mt * 128 * N))
+    with pytest.raises(ValueError, match="a_sf: needs at least"):
+        ctx.moe_gemm_mx(ctx.GEMM_F32, u8(mt * 128 * K), u8(mt * 128 * K // 32 - 4), None,
+                        u8(E * N * K // 2), u8(E * N * K // 32), i32(1), i32(mt), mt, E, N, K,
+                        torch.zeros(mt * 128 * N))
+    with pytest.raises(ValueError, match="below 2"):
+        ctx.moe_gemm_mx(ctx.GEMM_F32, u8(16), u8(16), None, u8(16), u8(16), i32(1), i32(1),
+                        4682, E, 256, 7168, torch.zeros(1))
+    # permute with the token count given: q / sf must hold that many rows
+    with pytest.raises(ValueError, match="q: needs at least"):
+        ctx.moe_permute_mx(u8(10 * 1024 - 1), u8(10 * 32), i32(8), i32(1), 1024, u8(8 * 1024),
+                           u8(8 * 32), tokens=10)
+    ctx.close()

@@ -124,7 +124,7 @@ def _chain(ctx, i, o):
     ctx.router_topk(i["S"], i["bias"], i["rs"], o["idx"], o["wts"], T, topk=TOPK)
     ctx.moe_route_count(o["idx"], T, RANK, E, o["bc"], topk=TOPK)
     ctx.moe_route_tables(o["bc"], NBLK, E, 128, o["bo"], o["cb"], o["cl"], o["nne"], o["tp"],
-                         o["rmap"])
+                         o["rmap"], T=T, topk=TOPK)
     ctx.moe_route_scatter(o["idx"], o["bo"], T, RANK, E, o["rmap"], o["e2p"], topk=TOPK)
     ctx.moe_permute_mx(o["q"], o["sf"], o["rmap"], o["tp"], H, o["pq"], o["psf"])
     ctx.land_add_attnres_rms_nb(i["partial"], i["prefix"], i["blocks"], i["sw"], i["gamma"],

@@ -12,7 +12,7 @@ import torch
 
 import k3h
 import oracle as O
-from k3data import bf16_to_f32, from_dev, normal_bf16, rng, to_dev, ulp_diff_bf16
+from k3data import bf16_to_f32, from_dev, normal_bf16, rng, to_bf16, to_dev, ulp_diff_bf16
 
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -100,21 +100,42 @@ def test_span_gather_split_spans_match_one_span(ctx):
     assert np.array_equal(w_split, w_one)
 
 
-@pytest.mark.parametrize("rows,at,span", [(16384, 0, 16384), (50, 9, 33)])
-def test_kda_out_gate(ctx, rows, at, span):
-    _case(f"kda_out_gate rows={rows} at={at} span={span}")
+@pytest.mark.parametrize("rows,at,span,eps,tiny", [
+    (16384, 0, 16384, 1e-6, False),   # config 3b as stated: eps 1e-6, attn ~N(0,1)
+    (16384, 0, 16384, 1e-5, False),
+    (50, 9, 33, 1e-6, True),          # heads of amplitude 1e-3: the norm's eps sets the result
+    (50, 9, 33, 1e-5, True),
+])
+def test_kda_out_gate(ctx, rows, at, span, eps, tiny):
+    _case(f"kda_out_gate rows={rows} at={at} span={span} eps={eps} tiny={tiny}")
     g = rng(2200 + span)
     attn = normal_bf16(g, (span, INNER))
+    if tiny:
+        a = bf16_to_f32(attn).reshape(span, HEADS, 128)
+        a[:, ::3] *= np.float32(1e-3)
+        attn = to_bf16(a.reshape(span, INNER))
     gate = normal_bf16(g, (rows, 4 * INNER))
     gamma_o = (1.0 + 0.1 * g.standard_normal(128)).astype(np.float32)
-    want = O.kda_out_gate(attn, gate, gamma_o, np.zeros((rows, INNER), np.uint16), at, span)
+    want = O.kda_out_gate(attn, gate, gamma_o, np.zeros((rows, INNER), np.uint16), at, span, eps=eps)
     gated = torch.zeros((rows, INNER), dtype=torch.bfloat16, device="cuda")
     ctx.kda_out_gate(to_dev(attn), to_dev(gate), to_dev(gamma_o), gated,
-                     to_dev(np.array([at], np.int32)), span)
+                     to_dev(np.array([at], np.int32)), span, eps=eps)
     torch.cuda.synchronize()
     got = from_dev(gated)
     _close1("gated", got[at:at + span], want[at:at + span])
     assert not got[:at].any() and not got[at + span:].any()
+    if tiny:
+        other = O.kda_out_gate(attn, gate, gamma_o, np.zeros((rows, INNER), np.uint16), at, span,
+                               eps=1e-5 if eps == 1e-6 else 1e-6)
+        assert (ulp_diff_bf16(got[at:at + span], other[at:at + span]) > 1).mean() > 0.1, \
+            "the other eps's module would have passed: eps not exercised"
+
+
+def test_kda_out_gate_rejects_other_eps(ctx):
+    with pytest.raises(ValueError, match="invalid argument"):
+        z = torch.zeros(4 * INNER, dtype=torch.bfloat16, device="cuda")
+        ctx.kda_out_gate(z, z, torch.ones(128, device="cuda"), z, to_dev(np.array([0], np.int32)),
+                         1, eps=1e-4)
 
 
 def test_manifest_kda_ops(ctx):

@@ -112,7 +112,7 @@ def _gpu_route(ctx, ids, T, topk):
     rmap = torch.full((cap,), -1, dtype=torch.int32, device="cuda")
     e2p = torch.empty(T * topk, dtype=torch.int32, device="cuda")
     ctx.moe_route_count(d_ids, T, RANK, E, bc, topk=topk)
-    ctx.moe_route_tables(bc, nblk, E, 128, bo, cb, cl, nne, tp, rmap)
+    ctx.moe_route_tables(bc, nblk, E, 128, bo, cb, cl, nne, tp, rmap, T=T, topk=topk)
     ctx.moe_route_scatter(d_ids, bo, T, RANK, E, rmap, e2p, topk=topk)
     torch.cuda.synchronize()
     return dict(bc=bc, bo=bo, cb=cb, cl=cl, nne=nne, tp=tp, rmap=rmap, e2p=e2p)

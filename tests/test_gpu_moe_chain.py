@@ -51,7 +51,7 @@ def test_moe_chain(ctx):
     rmap = torch.full((cap,), -1, dtype=torch.int32, device="cuda")
     e2p = torch.empty(T * TOPK, dtype=torch.int32, device="cuda")
     ctx.moe_route_count(idx, T, RANK, E, bc, topk=TOPK)
-    ctx.moe_route_tables(bc, nblk, E, 128, bo, cb, cl, nne, tp, rmap)
+    ctx.moe_route_tables(bc, nblk, E, 128, bo, cb, cl, nne, tp, rmap, T=T, topk=TOPK)
     ctx.moe_route_scatter(idx, bo, T, RANK, E, rmap, e2p, topk=TOPK)
     torch.cuda.synchronize()
     ids = from_dev(idx)

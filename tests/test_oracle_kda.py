@@ -2,6 +2,7 @@
 restatements (within one bf16 ulp), exact landing copies, and the window
 protocol's defining property -- a span of n rows equals n spans of one row."""
 import numpy as np
+import pytest
 import torch
 
 import oracle as O
@@ -51,19 +52,31 @@ def test_span_gather_span_of_n_equals_n_steps():
     assert np.array_equal(w2[:, 0], win[:, 2])
 
 
-def test_kda_out_gate_against_float64():
+@pytest.mark.parametrize("eps", [1e-5, 1e-6])
+def test_kda_out_gate_against_float64(eps):
+    """Against the float64 definition at both compiled eps values; a third of the
+    heads have amplitude 1e-3 (mean square ~1e-6), where the eps term sets the
+    norm, so a wrong eps fails."""
     rows, at, span = 20, 3, 12
     g = rng(210)
     attn = normal_bf16(g, (span, INNER))
+    a32 = bf16_to_f32(attn).reshape(span, HEADS, 128)
+    a32[:, ::3] *= np.float32(1e-3)
+    attn = to_bf16(a32.reshape(span, INNER))
     gate = normal_bf16(g, (rows, 4 * INNER))
     gamma_o = (1.0 + 0.1 * g.standard_normal(128)).astype(np.float32)
-    gated = O.kda_out_gate(attn, gate, gamma_o, np.zeros((rows, INNER), np.uint16), at, span)
+    gated = O.kda_out_gate(attn, gate, gamma_o, np.zeros((rows, INNER), np.uint16), at, span, eps=eps)
     a = bf16_to_f32(attn).astype(np.float64).reshape(span, HEADS, 128)
-    r = 1.0 / np.sqrt((a * a).mean(-1, keepdims=True) + 1e-5)
-    o = bf16_to_f32(to_bf16((a * r * gamma_o).astype(np.float32))).astype(np.float64)
     gg = bf16_to_f32(gate[at:at + span, 3 * INNER:]).astype(np.float64).reshape(span, HEADS, 128)
     gt = bf16_to_f32(to_bf16((1.0 / (1.0 + np.exp(-gg))).astype(np.float32))).astype(np.float64)
-    want = to_bf16((o * gt).reshape(span, INNER).astype(np.float32))
-    d = ulp_diff_bf16(gated[at:at + span], want)
+
+    def ref(e):
+        r = 1.0 / np.sqrt((a * a).mean(-1, keepdims=True) + e)
+        o = bf16_to_f32(to_bf16((a * r * gamma_o).astype(np.float32))).astype(np.float64)
+        return to_bf16((o * gt).reshape(span, INNER).astype(np.float32))
+
+    d = ulp_diff_bf16(gated[at:at + span], ref(eps))
     assert d.max() <= 1 and (d > 0).mean() < 2e-3
+    other = ulp_diff_bf16(gated[at:at + span], ref(1e-5 if eps == 1e-6 else 1e-6))
+    assert (other > 1).mean() > 0.1, "eps does not reach the result"
     assert not gated[:at].any() and not gated[at + span:].any()
