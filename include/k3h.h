@@ -183,6 +183,18 @@ K3H_API int k3h_quant_fp8_apply(k3h_ctx_t ctx, void* stream, int v2, const void*
                                 int n, const float* partials, int nb, float* scale_out);
 K3H_API int k3h_quant_fp8_tensor(k3h_ctx_t ctx, void* stream, int v2, const void* x, void* y,
                                  float* scale_out, float* partials, int n, int nb);
+/* k3h_quant_fp8_tensor_noalloc: no counterpart in the reference.  For callers
+ * that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): k3h_quant_fp8_tensor with the nb amax
+ * partials in a device array of this library (K3H_NOALLOC_MAX_NB floats, one
+ * copy per GPU, held until the process ends) instead of a caller buffer.  nb
+ * above K3H_NOALLOC_MAX_NB is K3H_EINVAL.  The first call on a device resolves
+ * the array's address (and, like every entry, loads the code object on first
+ * use); no call allocates device memory.  Every call on one GPU shares the
+ * array: calls that overlap on one GPU race and must be serialised. */
+#define K3H_NOALLOC_MAX_NB 4096
+K3H_API int k3h_quant_fp8_tensor_noalloc(k3h_ctx_t ctx, void* stream, int v2, const void* x,
+                                         void* y, float* scale_out, int n, int nb);
 
 /* k3h_residual_rms_mxfp8: fused residual add + RMSNorm + MXFP8 (no single
  * reference entry: K1b at nb = 0 composed with kern_k3_moe_quant).  Module

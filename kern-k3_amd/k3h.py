@@ -33,6 +33,7 @@ MOE_V4 = "k3_moe_prefill_v4+EP_RANKS=4+EP_STRIDED=1+TILE_SHIFT=7+SCATTER_WARPS=1
 MOE_V3 = "k3_moe_prefill_v3+EP_STRIDED=1"
 
 H = 7168
+NOALLOC_MAX_NB = 4096  # K3H_NOALLOC_MAX_NB of include/k3h.h
 
 
 class K3HError(RuntimeError):
@@ -69,6 +70,7 @@ _SIGS: dict[str, list] = {
     "k3h_quant_fp8_amax": [_P, _P, _I, _P, _I, _P, _I],
     "k3h_quant_fp8_apply": [_P, _P, _I, _P, _P, _I, _P, _I, _P],
     "k3h_quant_fp8_tensor": [_P, _P, _I, _P, _P, _P, _P, _I, _I],
+    "k3h_quant_fp8_tensor_noalloc": [_P, _P, _I, _P, _P, _P, _I, _I],
     "k3h_router_topk": [_P, _P, _I, _P, _P, _P, _P, _P, _I],
     "k3h_argmax_f32": [_P, _P, _P, _P, _P, _P, _I, _I, _I],
     "k3h_moe_route_count": [_P, _P, _I, _P, _I, _I, _I, _P],
@@ -416,6 +418,20 @@ class Ctx:
         _check(self.L.k3h_quant_fp8_tensor(self.h, _stream(stream), int(v2), _ptr(x), _ptr(y),
                                            _ptr(scale_out), _ptr(partials), n, nb),
                "quant_fp8_tensor")
+
+    def quant_fp8_tensor_noalloc(self, x, y, scale_out, n: int, nb: int = 2048, v2: bool = True,
+                                 stream=None) -> None:
+        """quant_fp8_tensor with the amax partials in the library's per-GPU device array
+        (no caller buffer, no allocation); nb <= NOALLOC_MAX_NB.  Calls that overlap on
+        one GPU share that array and race."""
+        if not 1 <= nb <= NOALLOC_MAX_NB:
+            raise ValueError(f"quant_fp8_tensor_noalloc: nb must be in [1, {NOALLOC_MAX_NB}]")
+        _dev(x, "x", BF16, n)
+        _dev(y, "y", U8, n, align=8)
+        _dev(scale_out, "scale_out", F32, 1, align=4)
+        _check(self.L.k3h_quant_fp8_tensor_noalloc(self.h, _stream(stream), int(v2), _ptr(x),
+                                                   _ptr(y), _ptr(scale_out), n, nb),
+               "quant_fp8_tensor_noalloc")
 
     def quant_fp8_amax(self, x, n: int, partials, v2: bool = True, stream=None) -> None:
         _dev(x, "x", BF16, n)
