@@ -363,6 +363,144 @@ def bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0) -> 
     return rows
 
 
+def bench_ceilings(ctx, out_path: str | None, reps: int = 100, flushed_reps: int = 30) -> list:
+    """Ceilings of this GPU (module k3h_probe): HBM rates of read-only, write-only,
+    copy and the fused op's 2-read : 1.5-write byte shape, over 235 MB streams,
+    with 1 or 4 coalesced 16-byte loads in flight per lane (flat grids), 4 or 8
+    (persistent grids, 8 workgroups per CU), non-temporal or cacheable; each
+    timed back to back (`reps` launches between two events, mean) and one launch
+    at a time after a 512 MB clean-read flush (median of `flushed_reps`).  Then
+    the register-to-register issue rate of v_mfma_scale_f32_32x32x64_f8f6f4 for
+    e4m3 x e2m1 (the MoE GEMMs' operands), e4m3 x e4m3 and e2m1 x e2m1.  The
+    fused op and the operators' stream copy run in the same process."""
+    import ctypes
+    import torch
+    import k3h
+    L = ctx.L
+    s = torch.cuda.current_stream()
+    n16 = T * H * 2 // 16
+    mk = lambda n: torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    a, b, c, d = mk(16 * n16), mk(16 * n16), mk(16 * n16), mk(8 * n16)
+    sink = torch.zeros(256, dtype=torch.int32, device="cuda")
+    flush_rd = torch.ones(128 << 20, dtype=torch.float32, device="cuda")
+    keep = []
+
+    def launcher(entry, grid, kinds, vals, block=256):
+        fn = ctx.function("k3h_probe", entry)
+        buf = k3h.pack_args(kinds, vals)
+        cbuf = ctypes.create_string_buffer(buf, len(buf))
+        g, bl = (ctypes.c_uint32 * 3)(grid, 1, 1), (ctypes.c_uint32 * 3)(block, 1, 1)
+        keep.append((cbuf, g, bl))
+
+        def go():
+            rc = L.k3h_launch(fn, g, bl, 0, s.cuda_stream, ctypes.cast(cbuf, ctypes.c_void_p), len(buf))
+            if rc:
+                raise k3h.K3HError(rc, entry)
+        return go
+
+    def time_it(fn, nrep, nflush):
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(nrep):
+            fn()
+        e1.record(s)
+        torch.cuda.synchronize()
+        b2b = e0.elapsed_time(e1) * 1e3 / nrep
+        ts = []
+        for _ in range(nflush):
+            flush_rd.sum()
+            e0.record(s)
+            fn()
+            e1.record(s)
+            e1.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e3)
+        ts.sort()
+        return b2b, ts[len(ts) // 2]
+
+    rows = []
+    P = "in buffer<u8>", "out buffer<u8>", "i64", "i32"
+    shapes = {  # op -> (bytes moved, kinds, values)
+        "read": (16 * n16, [P[0], P[2], P[1]], [a, n16, sink]),
+        "write": (16 * n16, [P[1], P[2], P[3]], [c, n16, 0x01010101]),
+        "copy": (32 * n16, [P[0], P[1], P[2]], [a, c, n16]),
+        "shape": (56 * n16, [P[0], P[0], P[1], P[1], P[2]], [a, b, c, d, n16]),
+    }
+    variants = [("u1", 1, None), ("u2", 2, None), ("u4", 4, None), ("u7", 7, None), ("u8", 8, None),
+                ("u4p", 4, 2048), ("u8p", 8, 2048), ("u4_c", 4, None)]
+    for op, (nbytes, kinds, vals) in shapes.items():
+        for suf, U, pgrid in variants:
+            grid = pgrid or n16 // (256 * U)
+            b2b, fl = time_it(launcher(f"k3h_probe_{op}_{suf}", grid, kinds, vals), reps, flushed_reps)
+            row = {"probe": f"{op}_{suf}", "op": op, "loads_in_flight": U,
+                   "grid": "persistent 2048" if pgrid else f"flat {grid}",
+                   "cache": "cacheable" if suf.endswith("_c") else "non-temporal",
+                   "bytes": nbytes, "us_b2b": round(b2b, 2), "gbs_b2b": round(nbytes / b2b / 1e3, 1),
+                   "us_flushed": round(fl, 2), "gbs_flushed": round(nbytes / fl / 1e3, 1)}
+            rows.append(row)
+            log(f"{row['probe']:12s} {b2b:8.2f} us {row['gbs_b2b']:7.0f} GB/s back to back | "
+                f"{fl:8.2f} us {row['gbs_flushed']:7.0f} GB/s flushed")
+    # the operators' copy and the fused op, same process
+    ta = a.view(torch.bfloat16)
+    tc = c.view(torch.bfloat16)
+    b2b, fl = time_it(lambda: ctx.stream_copy(ta, tc, stream=s), reps, flushed_reps)
+    rows.append({"probe": "k3h_stream_copy (operators' module)", "op": "copy", "loads_in_flight": 1,
+                 "grid": f"flat {n16 // 256}", "cache": "non-temporal", "bytes": 32 * n16,
+                 "us_b2b": round(b2b, 2), "gbs_b2b": round(32 * n16 / b2b / 1e3, 1),
+                 "us_flushed": round(fl, 2), "gbs_flushed": round(32 * n16 / fl / 1e3, 1)})
+    del a, b, c, d
+    x, res, gm = make_inputs(T)
+    ro = torch.empty_like(x)
+    q = torch.empty((T, H), dtype=torch.uint8, device="cuda")
+    sf = torch.empty((T, H // 32), dtype=torch.uint8, device="cuda")
+    nb = algo_bytes(T)
+    b2b, fl = time_it(lambda: ctx.residual_rms_mxfp8(x, res, gm, ro, q, sf, None, eps=1e-6, B=T,
+                                                     stream=s), reps, flushed_reps)
+    rows.append({"probe": "k3h_residual_rms_mxfp8 (the fused op)", "op": "shape", "loads_in_flight": 14,
+                 "grid": f"flat {T // 2}", "cache": "non-temporal", "bytes": nb,
+                 "us_b2b": round(b2b, 2), "gbs_b2b": round(nb / b2b / 1e3, 1),
+                 "us_flushed": round(fl, 2), "gbs_flushed": round(nb / fl / 1e3, 1)})
+    del x, res, gm, ro, q, sf
+    # MFMA issue rate, register operands
+    n_wg, iters = 256 * 2, 2000
+    mout = torch.empty(n_wg * 256, dtype=torch.float32, device="cuda")
+    for fmt in ("f8f4", "f8f8", "f4f4"):
+        fn = launcher(f"k3h_probe_mfma_{fmt}", n_wg, ["out buffer<f32>", "i32"], [mout, iters])
+        b2b, _ = time_it(fn, 20, 1)
+        flops = n_wg * 4 * iters * 4 * 131072
+        rows.append({"probe": f"mfma_{fmt}", "op": "mfma", "grid": f"{n_wg} x 256",
+                     "flops": flops, "us_b2b": round(b2b, 2),
+                     "tflops": round(flops / b2b / 1e6, 1)})
+        log(f"mfma {fmt}: {b2b:.1f} us, {flops / b2b / 1e6:.0f} TFLOP/s")
+    if out_path:
+        with open(out_path, "w") as f:
+            json.dump(rows, f, indent=1)
+    return rows
+
+
+def ceilings_markdown(rows: list) -> str:
+    out = ["| probe | access | loads in flight per lane | grid | bytes | back to back us | GB/s | % of 8 TB/s "
+           "| flushed us | GB/s | % of 8 TB/s |",
+           "|---|---|---:|---|---:|---:|---:|---:|---:|---:|---:|"]
+    for r in rows:
+        if r["op"] == "mfma":
+            continue
+        out.append(f"| {r['probe']} | {r['op']}, {r['cache']} | {r['loads_in_flight']} | {r['grid']} | "
+                   f"{r['bytes']:,} | {r['us_b2b']:.2f} | {r['gbs_b2b']:.0f} | "
+                   f"{100 * r['gbs_b2b'] / PEAK_GBS:.1f} | {r['us_flushed']:.2f} | {r['gbs_flushed']:.0f} | "
+                   f"{100 * r['gbs_flushed'] / PEAK_GBS:.1f} |")
+    out += ["", "| MFMA probe | operands (A x B) | grid | FLOPs per launch | us | TFLOP/s |",
+            "|---|---|---|---:|---:|---:|"]
+    names = {"mfma_f8f4": "e4m3 x e2m1", "mfma_f8f8": "e4m3 x e4m3", "mfma_f4f4": "e2m1 x e2m1"}
+    for r in rows:
+        if r["op"] == "mfma":
+            out.append(f"| {r['probe']} | {names[r['probe']]} | {r['grid']} | {r['flops']:,} | "
+                       f"{r['us_b2b']:.1f} | {r['tflops']:.0f} |")
+    return "\n".join(out)
+
+
 def cpu_route(O, ids, T, nblk, E, cap) -> None:
     """The oracle's count -> tables -> scatter chain for EP rank 0 (CPU baseline)."""
     bc = O.route_count(ids, T, 8, 0, E)
@@ -685,8 +823,12 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--flushed-reps", type=int, default=50,
                     help="launches timed one by one after a cache flush (the 'flushed' record)")
-    ap.add_argument("--op", choices=["fused", "copy"], default="fused",
-                    help="copy: only the 16-byte streaming copy (counter calibration)")
+    ap.add_argument("--op", choices=["fused", "copy", "ceilings"], default="fused",
+                    help="copy: only the 16-byte streaming copy (counter calibration); "
+                         "ceilings: HBM access-shape and MFMA-rate probes (markdown on stdout)")
+    ap.add_argument("--ceilings-out", default=None, help="write the ceilings rows as JSON")
+    ap.add_argument("--ceilings-table", metavar="CEILINGS_JSON",
+                    help="print the markdown table of a --ceilings-out JSON; no GPU")
     ap.add_argument("--ops", action="store_true",
                     help="also time every op at its config shape (table on stderr)")
     ap.add_argument("--ops-only", action="store_true", help="only the per-op table")
@@ -703,6 +845,9 @@ def main() -> int:
     if a.ops_table:
         print(ops_markdown(a.ops_table))
         return 0
+    if a.ceilings_table:
+        print(ceilings_markdown(json.load(open(a.ceilings_table))))
+        return 0
     if a.gpus != 1:
         print(f"bench.py measures one GPU only (asked for {a.gpus}); the op family shards "
               "by rows / heads / experts with no exchange on the measured path.", file=sys.stderr)
@@ -713,6 +858,9 @@ def main() -> int:
 
     ctx = k3h.Ctx()
     rows = a.rows
+    if a.op == "ceilings":
+        print(ceilings_markdown(bench_ceilings(ctx, a.ceilings_out)), flush=True)
+        return 0
     if a.ops_only:
         bench_ops(ctx, max(5, a.steps), a.ops_out, 0.0 if a.no_cpu else 3.0)
         return 0

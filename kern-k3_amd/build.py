@@ -53,6 +53,7 @@ SOURCES = {
     "k3_situ_bf16": "k3_land.hip",
     "k3_land_fused": "k3_land.hip",
     "k3h_moe_gemm": "k3h_moe_gemm.hip",
+    "k3h_probe": "k3h_probe.hip",
 }
 
 # defines implied by a base name that shares its source with another base
@@ -101,6 +102,7 @@ MODULES = [
     "k3_situ_bf16",
     "k3_land_fused",
     "k3h_moe_gemm",
+    "k3h_probe",
 ]
 
 DEVICE_FLAGS = [

@@ -83,3 +83,18 @@ def test_ops_markdown_columns(tmp_path):
     assert cells[14] == f"{rows[1]['gbs'] / rows[1]['cpu_gbs']:.0f}x"
     assert any(l.startswith("| MoE fc2") for l in md)                    # MFMA table
     assert not any(l.startswith("| MoE fc2") and "629" in l for l in md)
+
+
+def test_ceilings_markdown_rates():
+    rows = [
+        {"probe": "copy_u4", "op": "copy", "loads_in_flight": 4, "grid": "flat 16", "cache": "non-temporal",
+         "bytes": 8_000_000, "us_b2b": 2.0, "gbs_b2b": 4000.0, "us_flushed": 4.0, "gbs_flushed": 2000.0},
+        {"probe": "mfma_f8f4", "op": "mfma", "grid": "2 x 256", "flops": 10_000_000, "us_b2b": 2.0,
+         "tflops": 5.0},
+    ]
+    md = bench.ceilings_markdown(rows).splitlines()
+    copy = [c.strip() for c in next(l for l in md if l.startswith("| copy_u4")).strip("|").split("|")]
+    assert copy[1] == "copy, non-temporal" and copy[6] == "4000" and copy[7] == "50.0"  # % of 8 TB/s
+    assert copy[9] == "2000" and copy[10] == "25.0"
+    mf = [c.strip() for c in next(l for l in md if l.startswith("| mfma_f8f4")).strip("|").split("|")]
+    assert mf[1] == "e4m3 x e2m1" and mf[5] == "5"
