@@ -190,6 +190,16 @@ K3_DEV float k3_sigmoid(float x) {
   return 1.0f / (1.0f + k3_expf(t < -87.0f ? -87.0f : t));
 }
 
+// k3_sigmoid without a branch (same bits for every input, NaN included): the
+// overflow side is evaluated on a clamped argument and selected away.
+K3_DEV float k3_sigmoid_nb(float x) {
+  const float t = -x;
+  const bool over = t >= 0x1.62e430p+6f;
+  const float tc = over ? 0.0f : (t < -87.0f ? -87.0f : t);
+  const float r = 1.0f / (1.0f + k3_expf(tc));
+  return over ? 0.0f : r;
+}
+
 // Fast logistic for bf16-landed inputs: hardware 2^x and reciprocal
 // (v_exp_f32, v_rcp_f32), about 1 ulp each; results are rounded to bf16.
 K3_DEV float k3_sigmoid_fast(float x) {
