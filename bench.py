@@ -327,6 +327,13 @@ def bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0) -> 
         f"T={T} top-8 E=56", 2 * T * 8 * 4 + 3 * nblk * E * 4 + tpad * 4, t_route,
         "latency-bound (three launches, one single-workgroup scan)",
         cpu=O and (lambda a=h(idx): cpu_route(O, a, T, nblk, E, cap)))
+    sync = torch.zeros(2, dtype=torch.int32, device="cuda")
+    add("EP routing, one launch (k3h_moe_route)", "k3h_moe_route_fused", f"T={T} top-8 E=56",
+        2 * T * 8 * 4 + 3 * nblk * E * 4 + tpad * 4,
+        timed(lambda: ctx.moe_route(idx, T, 0, E, bc, bo, cb, cl, nne, tp, rmap, e2p, sync, topk=8,
+                                    stream=s)),
+        "latency-bound (one launch, one grid barrier)",
+        cpu=O and (lambda a=h(idx): cpu_route(O, a, T, nblk, E, cap)))
     x8 = torch.randint(0, 256, (T, H), dtype=torch.uint8, device="cuda", generator=g)
     sf8 = torch.randint(0, 256, (T, H // 32), dtype=torch.uint8, device="cuda", generator=g)
     pq = torch.empty((tpad, H), dtype=torch.uint8, device="cuda")
@@ -649,6 +656,7 @@ OP_KERNELS = {
     "router top-8 (cfg 5a)": ["k3h_router_topk_rows"],
     "EP routing tables (count+tables+scatter)": ["kern_k3_moe_route_count", "kern_k3_moe_route_tables",
                                                  "kern_k3_moe_route_scatter"],
+    "EP routing, one launch (k3h_moe_route)": ["k3h_moe_route_fused"],
     "MXFP8 permute (cfg 5c)": ["k3h_moe_permute_mx"],
     "weighted finalize (cfg 5d)": ["kern_k3_moe_finalize"],
     "residual push v3 (res_in, nb 0, 4 ranks)": ["kern_k3_attnres_rms_push"],

@@ -231,6 +231,22 @@ K3H_API int k3h_moe_route_tables(k3h_ctx_t ctx, void* stream, const int* blockco
 K3H_API int k3h_moe_route_scatter(k3h_ctx_t ctx, void* stream, int topk, const int* ids,
                                   const int* blockoff, int T, int rank, int E, int* route_map,
                                   int* exp2perm);
+/* k3h_moe_route: no reference entry (the reference runs route_count,
+ * route_tables and route_scatter as three launches).  The same outputs as that
+ * chain -- blockcount, blockoff, cta_batch, cta_limit, num_non_exiting,
+ * total_padded, route_map, exp2perm, bit for bit -- from one launch of
+ * k3h_moe_route_fused (module k3_moe_prefill_v4+...[+TOPK=8]; grid
+ * ceil(T / 256) <= 256, i.e. T <= 65536, block 512), whose workgroups meet at
+ * one grid barrier.  sync: 2 ints of device memory, zero before the first call;
+ * each call leaves them zero again.  Calls that share `sync` must not overlap
+ * (stream-order them).  The barrier's wait is bounded: if it expires (only
+ * possible when the grid cannot be resident at once) total_padded is -1 and
+ * the other outputs are incomplete.  T = 0 writes num_non_exiting =
+ * total_padded = 0. */
+K3H_API int k3h_moe_route(k3h_ctx_t ctx, void* stream, int topk, const int* ids, int T, int rank,
+                          int E, int* blockcount, int* blockoff, int* cta_batch, int* cta_limit,
+                          int* num_non_exiting, int* total_padded, int* route_map, int* exp2perm,
+                          int* sync);
 /* kern_k3_moe_finalize (k3_moe_prefill_v4.cu:254; op moe_finalize, json:405686):
  * fc2 bf16 [total_padded, cols], wts f32 [T,topk] -> out bf16 [T, cols].
  * grid ceil(T/2), block 128; cols % 8 == 0. */

@@ -13,6 +13,7 @@
 namespace {
 constexpr int kExperts = 224;
 constexpr int kMaxE = 64;
+constexpr int kRouteMaxBlocks = 256;  // RF_MAX_BLOCKS of k3h_moe_route_fused
 const char* kMoeV4 = "k3_moe_prefill_v4+EP_RANKS=4+EP_STRIDED=1+TILE_SHIFT=7+SCATTER_WARPS=16";
 
 bool topk_key(const char* base, int topk, std::string* key) {
@@ -96,6 +97,29 @@ K3H_API int k3h_moe_route_scatter(k3h_ctx_t ctx, void* stream, int topk, const i
   a.ptr(ids).ptr(blockoff).i32(T).i32(rank).i32(E).ptr(route_map).ptr(exp2perm);
   return k3h_run(ctx, key.c_str(), "kern_k3_moe_route_scatter", k3h_cdiv(T, 256), 1, 1, 512,
                  stream, a);
+}
+
+K3H_API int k3h_moe_route(k3h_ctx_t ctx, void* stream, int topk, const int* ids, int T, int rank,
+                          int E, int* blockcount, int* blockoff, int* cta_batch, int* cta_limit,
+                          int* num_non_exiting, int* total_padded, int* route_map, int* exp2perm,
+                          int* sync) {
+  std::string key;
+  if (!ctx || T < 0 || E < 1 || E > kMaxE || rank < 0 || !topk_key(kMoeV4, topk, &key))
+    return K3H_EINVAL;
+  const int blocks = (int)k3h_cdiv(T, 256);
+  if (blocks > kRouteMaxBlocks) return K3H_EINVAL;
+  if (!k3h_okp(blockcount, 4) || !k3h_okp(blockoff, 4) || !k3h_okp(cta_batch, 4) ||
+      !k3h_okp(cta_limit, 4) || !k3h_okp(num_non_exiting, 4) || !k3h_okp(total_padded, 4) ||
+      !k3h_okp(route_map, 4) || (T > 0 && !k3h_okp(ids, 4)) || (T > 0 && !k3h_okp(exp2perm, 4)) ||
+      !k3h_okp(sync, 4))
+    return K3H_EINVAL;
+  if (T == 0)  // no ids: the tables of zero blocks (num_non_exiting = total_padded = 0)
+    return k3h_moe_route_tables(ctx, stream, blockcount, 0, E, 128, blockoff, cta_batch, cta_limit,
+                                num_non_exiting, total_padded, route_map);
+  K3hArgs a;
+  a.ptr(ids).i32(T).i32(rank).i32(E).ptr(blockcount).ptr(blockoff).ptr(cta_batch).ptr(cta_limit);
+  a.ptr(num_non_exiting).ptr(total_padded).ptr(route_map).ptr(exp2perm).ptr(sync);
+  return k3h_run(ctx, key.c_str(), "k3h_moe_route_fused", (uint32_t)blocks, 1, 1, 512, stream, a);
 }
 
 K3H_API int k3h_moe_finalize(k3h_ctx_t ctx, void* stream, int topk, const void* fc2,

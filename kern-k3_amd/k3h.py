@@ -76,6 +76,7 @@ _SIGS: dict[str, list] = {
     "k3h_moe_route_count": [_P, _P, _I, _P, _I, _I, _I, _P],
     "k3h_moe_route_tables": [_P, _P, _P, _I, _I, _I, _P, _P, _P, _P, _P, _P],
     "k3h_moe_route_scatter": [_P, _P, _I, _P, _P, _I, _I, _I, _P, _P],
+    "k3h_moe_route": [_P, _P, _I, _P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P],
     "k3h_moe_finalize": [_P, _P, _I, _P, _P, _P, _P, _I, _I],
     "k3h_moe_permute_mx": [_P, _P, _P, _P, _P, _P, _I, _I, _P, _P],
     "k3h_moe_w_shuffle": [_P, _P, _P, _P, _I, _I, _I, _I],
@@ -498,6 +499,31 @@ class Ctx:
         _check(self.L.k3h_moe_route_scatter(self.h, _stream(stream), topk, _ptr(ids), _ptr(blockoff),
                                             T, rank, E, _ptr(route_map), _ptr(exp2perm)),
                "moe_route_scatter")
+
+    def moe_route(self, ids, T: int, rank: int, E: int, blockcount, blockoff, cta_batch, cta_limit,
+                  num_non_exiting, total_padded, route_map, exp2perm, sync, topk: int = 16,
+                  stream=None) -> None:
+        """route_count -> route_tables -> route_scatter in one launch (T <= 65536).
+        sync: 2 int32 zeroed before the first call (each call leaves them zero)."""
+        blocks = -(-T // 256)
+        max_tiles = (T * topk + 127 * E) // 128 if T > 0 else 0  # T = 0 writes no table row
+        if blocks > 256:
+            raise ValueError("moe_route: T above 65536 (use the three-launch chain)")
+        if T > 0:
+            _dev(ids, "ids", I32, T * topk, align=4)
+            _dev(exp2perm, "exp2perm", I32, T * topk, align=4)
+        _dev(blockcount, "blockcount", I32, blocks * E, align=4)
+        _dev(blockoff, "blockoff", I32, blocks * E, align=4)
+        _dev(cta_batch, "cta_batch", I32, max(1, max_tiles), align=4)
+        _dev(cta_limit, "cta_limit", I32, max(1, max_tiles), align=4)
+        _dev(num_non_exiting, "num_non_exiting", I32, 1, align=4)
+        _dev(total_padded, "total_padded", I32, 1, align=4)
+        _dev(route_map, "route_map", I32, max(1, max_tiles * 128), align=4)
+        _dev(sync, "sync", I32, 2, align=4)
+        _check(self.L.k3h_moe_route(self.h, _stream(stream), topk, _ptr(ids), T, rank, E,
+                                    _ptr(blockcount), _ptr(blockoff), _ptr(cta_batch),
+                                    _ptr(cta_limit), _ptr(num_non_exiting), _ptr(total_padded),
+                                    _ptr(route_map), _ptr(exp2perm), _ptr(sync)), "moe_route")
 
     def moe_finalize(self, fc2, exp2perm, wts, out, T: int, cols: int, topk: int = 16,
                      stream=None) -> None:

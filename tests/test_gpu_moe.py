@@ -139,6 +139,57 @@ def test_ep_routing_tables(ctx, T, topk):
     _eq("exp2perm", from_dev(d["e2p"]), e2p)
 
 
+# one launch of k3h_moe_route against the oracle's chain; each case runs twice on
+# one `sync` (the barrier words must come back zero); T = 1 and T = 65536 are the
+# smallest and largest grids of the one-launch path
+@pytest.mark.parametrize("T,topk", [(16384, 8), (16384, 16), (300, 16), (257, 8), (40000, 8),
+                                    (1, 8), (65536, 8)])
+def test_route_one_launch(ctx, T, topk):
+    _case(f"one-launch routing T={T} topk={topk}")
+    S, bias, rs = _router_inputs(T, 1700 + T + topk)
+    ids, _ = O.router_topk(S, bias, rs[0], T, topk)
+    nblk = (T + 255) // 256
+    bc = O.route_count(ids, T, topk, RANK, E)
+    cap = T * topk + E * 128
+    tab = O.route_tables(bc, nblk, E, 128, cap)
+    rmap, e2p = O.route_scatter(ids, tab["blockoff"], T, topk, RANK, E, tab["route_map"])
+    nne, tp = tab["num_non_exiting"], tab["total_padded"]
+    d_ids = to_dev(ids)
+    sync = torch.zeros(2, dtype=torch.int32, device="cuda")
+    for rep in range(2):
+        o = dict(bc=torch.full((nblk * E,), -7, dtype=torch.int32, device="cuda"),
+                 bo=torch.full((nblk * E,), -7, dtype=torch.int32, device="cuda"),
+                 cb=torch.full((cap // 128 + 1,), -7, dtype=torch.int32, device="cuda"),
+                 cl=torch.full((cap // 128 + 1,), -7, dtype=torch.int32, device="cuda"),
+                 nne=torch.full((1,), -7, dtype=torch.int32, device="cuda"),
+                 tp=torch.full((1,), -7, dtype=torch.int32, device="cuda"),
+                 rmap=torch.full((cap,), -7, dtype=torch.int32, device="cuda"),
+                 e2p=torch.full((T * topk,), -7, dtype=torch.int32, device="cuda"))
+        ctx.moe_route(d_ids, T, RANK, E, o["bc"], o["bo"], o["cb"], o["cl"], o["nne"], o["tp"],
+                      o["rmap"], o["e2p"], sync, topk=topk)
+        torch.cuda.synchronize()
+        assert from_dev(sync).tolist() == [0, 0], "barrier words not reset"
+        _eq("blockcount", from_dev(o["bc"]), bc)
+        _eq("blockoff", from_dev(o["bo"]), tab["blockoff"])
+        assert from_dev(o["nne"])[0] == nne and from_dev(o["tp"])[0] == tp
+        _eq("cta_batch", from_dev(o["cb"])[:nne], tab["cta_batch"][:nne])
+        _eq("cta_limit", from_dev(o["cl"])[:nne], tab["cta_limit"][:nne])
+        _eq("route_map", from_dev(o["rmap"])[:tp], rmap[:tp])
+        assert (from_dev(o["rmap"])[tp:] == -7).all(), "rows past total_padded written"
+        _eq("exp2perm", from_dev(o["e2p"]), e2p)
+
+
+def test_route_one_launch_empty_and_limits(ctx):
+    z = torch.zeros(64, dtype=torch.int32, device="cuda")
+    nne = torch.full((1,), -7, dtype=torch.int32, device="cuda")
+    tp = torch.full((1,), -7, dtype=torch.int32, device="cuda")
+    ctx.moe_route(z, 0, RANK, E, z, z, z, z, nne, tp, z, z, z[:2], topk=8)
+    torch.cuda.synchronize()
+    assert nne.item() == 0 and tp.item() == 0
+    with pytest.raises(ValueError):
+        ctx.moe_route(z, 65537, RANK, E, z, z, z, z, nne, tp, z, z, z[:2], topk=8)
+
+
 def test_permute_and_finalize_config5(ctx):
     """Config 5: 16384 tokens, top-8 of 224, EP rank 0 of 4 (56 local experts):
     router -> tables -> MXFP8 permute of the quantised activations -> finalize of
