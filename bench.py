@@ -749,6 +749,50 @@ def traffic_table(fetch_csv: str, write_csv: str, ops_json: str) -> str:
     return "\n".join(out)
 
 
+def trace_table(trace_csv: str, ops_json: str) -> str:
+    """Markdown table of kernel-trace durations per op: from a rocprofv3
+    --kernel-trace CSV of a bench.py --ops-only run and that run's --ops-out JSON,
+    each op's dispatches are taken in launch order (5 warm-ups, then `reps` after
+    the clean-read flush, then `reps` after the dirty flush); an op's time per
+    launch is the sum of its kernels' spans; the median over the clean-flush
+    launches is set beside the HIP-event median of the same launches (which also
+    holds the launch itself)."""
+    per = {}
+    for r in _csv_rows(trace_csv):
+        name = _col(r, "Kernel_Name").split("(")[0].strip()
+        span = (int(_col(r, "End_Timestamp")) - int(_col(r, "Start_Timestamp"))) / 1e3
+        per.setdefault(name, []).append((int(_col(r, "Dispatch_Id")), span))
+    per = {k: [d for _, d in sorted(v)] for k, v in per.items()}
+    pos = {k: 0 for k in per}
+    ops = {r["op"]: r for r in json.load(open(ops_json))}
+    out = ["| op | kernels | HIP-event median us | kernel median us | GB/s (kernel time) | % of 8 TB/s "
+           "| TFLOP/s (kernel time) |", "|---|---|---:|---:|---:|---:|---:|"]
+    for op, kernels in OP_KERNELS.items():
+        if op not in ops:
+            continue
+        r = ops[op]
+        n = r.get("launches", 0)
+        reps = (n - 5) // 2
+        runs = []
+        for k in kernels:
+            if k not in per:
+                runs = None
+                break
+            runs.append(per[k][pos[k]:pos[k] + n])
+            pos[k] += n
+        if not runs or any(len(x) < n for x in runs):
+            continue
+        clean = sorted(sum(x[i] for x in runs) for i in range(5, 5 + reps))
+        us = clean[len(clean) // 2]
+        if r.get("bound") == "mfma":
+            rate = f" | | {r['flops'] / (us * 1e-6) / 1e12:.1f}"
+        else:
+            gbs = r["bytes"] / (us * 1e-6) / 1e9
+            rate = f" | {gbs:.1f} | {100 * gbs / PEAK_GBS:.1f} | "
+        out.append(f"| {op} | {', '.join('`%s`' % k for k in kernels)} | {r['us']:.2f} | {us:.2f}{rate} |")
+    return "\n".join(out)
+
+
 def ops_markdown(ops_json: str) -> str:
     """Markdown tables of a bench.py --ops-out JSON: the HBM-bound ops (GB/s, % of
     8 TB/s, % of the run's copy ceiling, CPU oracle column where timed) and the
@@ -843,12 +887,18 @@ def main() -> int:
     ap.add_argument("--ops-out", default=None, help="write the per-op table as JSON")
     ap.add_argument("--ops-table", metavar="OPS_JSON",
                     help="print the per-op markdown table of an --ops-out JSON; no GPU")
+    ap.add_argument("--trace-table", nargs=2, metavar=("TRACE_CSV", "OPS_JSON"),
+                    help="print per-op kernel-trace medians (clean-flush launches) from a rocprofv3 "
+                         "--kernel-trace CSV of --ops-only and its --ops-out JSON; no GPU")
     ap.add_argument("--traffic-table", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "OPS_JSON"),
                     help="print the per-op HBM byte table from two rocprofv3 --pmc CSVs "
                          "(FETCH_SIZE, WRITE_SIZE runs of --ops-only) and an --ops-out JSON; no GPU")
     a = ap.parse_args()
     if a.traffic_table:
         print(traffic_table(*a.traffic_table))
+        return 0
+    if a.trace_table:
+        print(trace_table(*a.trace_table))
         return 0
     if a.ops_table:
         print(ops_markdown(a.ops_table))

@@ -98,3 +98,32 @@ def test_ceilings_markdown_rates():
     assert copy[9] == "2000" and copy[10] == "25.0"
     mf = [c.strip() for c in next(l for l in md if l.startswith("| mfma_f8f4")).strip("|").split("|")]
     assert mf[1] == "e4m3 x e2m1" and mf[5] == "5"
+
+
+def test_trace_table_takes_clean_flush_launches(tmp_path):
+    """Dispatch order per kernel: 5 warm-ups, reps clean, reps dirty; multi-kernel
+    ops sum their kernels per launch."""
+    reps = 3
+    ops = [{"op": "stream copy (ceiling)", "kernel": "k3h_stream_copy", "bytes": 8_000_000,
+            "launches": 5 + 2 * reps, "us": 9.0},
+           {"op": "EP routing tables (count+tables+scatter)", "kernel": "x", "bytes": 1_000,
+            "launches": 5 + 2 * reps, "us": 20.0}]
+    json.dump(ops, open(tmp_path / "ops.json", "w"))
+    spans = {"k3h_stream_copy": [1] * 5 + [2, 4, 3] + [50] * 3,
+             "kern_k3_moe_route_count": [1] * 5 + [1, 1, 1] + [9] * 3,
+             "kern_k3_moe_route_tables": [1] * 5 + [2, 2, 2] + [9] * 3,
+             "kern_k3_moe_route_scatter": [1] * 5 + [3, 5, 4] + [9] * 3}
+    with open(tmp_path / "tr.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Dispatch_Id", "Kernel_Name", "Start_Timestamp", "End_Timestamp"])
+        w.writeheader()
+        did = 0
+        for i in range(5 + 2 * reps):  # interleaved dispatch ids, as in a real trace
+            for k, v in spans.items():
+                did += 1
+                w.writerow({"Dispatch_Id": did, "Kernel_Name": k + "(int*)", "Start_Timestamp": 1000,
+                            "End_Timestamp": 1000 + int(v[i] * 1000)})
+    md = bench.trace_table(str(tmp_path / "tr.csv"), str(tmp_path / "ops.json")).splitlines()
+    cp = [c.strip() for c in next(l for l in md if l.startswith("| stream copy")).strip("|").split("|")]
+    assert cp[3] == "3.00" and cp[4] == f"{8_000_000 / 3e-6 / 1e9:.1f}"   # median of 2, 4, 3
+    rt = [c.strip() for c in next(l for l in md if l.startswith("| EP routing tables")).strip("|").split("|")]
+    assert rt[3] == "7.00"                                                # 1+2+4 (median of 6, 8, 7)
