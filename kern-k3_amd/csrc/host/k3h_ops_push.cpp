@@ -106,12 +106,14 @@ K3H_API int k3h_land_add_attnres_rms_nb_stats(k3h_ctx_t ctx, void* stream, const
   if (!snapshot && !k3h_okp(prefix, 16)) return K3H_EINVAL;
   if (nb_stats > 0 && !k3h_okp(stats, 8)) return K3H_EINVAL;
   if (B == 0) return K3H_OK;
-  const std::string entry = "kern_k3_land_add_attnres_rms_nb" + std::to_string(nb);
+  const bool split = nb <= kSplitNbMax;
+  const std::string entry = (split ? "k3h_land_add_attnres_rms_nb" : "kern_k3_land_add_attnres_rms_nb") +
+                            std::to_string(nb) + (split ? "s" : "");
   K3hArgs a;
   a.ptr(partial).ptr(prefix).ptr(blocks).ptr(sw).ptr(gamma).ptr(prefix2).ptr(normed);
   a.i32(nb).i32(snapshot).i32(B).ptr(stats).i32(nb_stats);
   return k3h_run(ctx, "k3_residual_nb_stats", entry.c_str(), (uint32_t)B, 1, 1,
-                 kResThreads, stream, a);
+                 split ? kSplitThreads : kResThreads, stream, a);
 }
 
 K3H_API int k3h_land_add2_bf16(k3h_ctx_t ctx, void* stream, const void* p1, const void* p2,

@@ -73,12 +73,16 @@ K3H_API int k3h_land_add_attnres_rms_nb(k3h_ctx_t ctx, void* stream, const void*
   if (!k3h_okp(partial, 16) || !k3h_okp(prefix2, 16)) return K3H_EINVAL;
   if (!snapshot && !k3h_okp(prefix, 16)) return K3H_EINVAL;
   if (B == 0) return K3H_OK;
-  const std::string entry = "kern_k3_land_add_attnres_rms_nb" + std::to_string(nb);
+  // nb <= kSplitNbMax: the 256-thread vector-split entry (same outputs, every
+  // candidate held on chip); above, the manifest's 128-thread entry
+  const bool split = nb <= kSplitNbMax;
+  const std::string entry = (split ? "k3h_land_add_attnres_rms_nb" : "kern_k3_land_add_attnres_rms_nb") +
+                            std::to_string(nb) + (split ? "s" : "");
   K3hArgs a;
   a.ptr(partial).ptr(prefix).ptr(blocks).ptr(sw).ptr(gamma).ptr(prefix2).ptr(normed);
   a.i32(nb).i32(snapshot).i32(B);
   return k3h_run(ctx, "k3_residual_nb+LAND_BF16=1", entry.c_str(), (uint32_t)B, 1, 1,
-                 kResThreads, stream, a);
+                 split ? kSplitThreads : kResThreads, stream, a);
 }
 
 K3H_API int k3h_attnres_rms(k3h_ctx_t ctx, void* stream, const void* prefix, void* blocks,

@@ -17,7 +17,7 @@
 // stats[b] ([B, 8, 2] f32, written by res_in's push-stats entry) instead of a
 // pass over their rows (k3_residual_nb_stats.cu:176-258, 366-811; manifest ops
 // land_add_attnres_rms_bf16_v2_nb4..8).  nb_stats is clamped to [0, nb].
-#include "k3_residual_row.h"
+#include "k3_residual_split.h"
 
 #ifndef K3_NB_STATS
 #define K3_NB_ENTRY(K)                                                                      \
@@ -46,6 +46,47 @@
                                                      nb_stats);                               \
   }
 #endif
+
+// Typed-call entries with no reference counterpart: the same contract on the
+// vector-split row body (k3_residual_split.h), grid (B, 1, 1), block 256:
+//   k3h_land_add_attnres_rms_nb{1..5}s(..., nb_in, snapshot, B[, stats, nb_stats])
+// Measured at B = 4096, cold caches, against the 128-thread entries: nb 1-5
+// 58.3 / 69.0 / 82.8 / 97.2 / 107.7 -> 56.8 / 65.1 / 76.1 / 85.7 / 95.8 us; from
+// nb 6 on the candidates need more than half a SIMD's registers per wave and
+// the split form runs slower (nb 8: 151 -> 220 us), so it is not built there.
+#ifndef K3_NB_STATS
+#define K3_NBS_ENTRY(K)                                                                     \
+  extern "C" __global__ void __launch_bounds__(K3S_THREADS)                              \
+      k3h_land_add_attnres_rms_nb##K##s(                                                    \
+          const k3_land_t* __restrict__ partial, const uint16_t* __restrict__ prefix,       \
+          const uint16_t* __restrict__ blocks, const float* __restrict__ sw,                \
+          const uint16_t* __restrict__ gamma, uint16_t* __restrict__ prefix2,               \
+          uint16_t* __restrict__ normed, int nb_in, int snapshot, int B) {                  \
+    if (nb_in != K) return;                                                                 \
+    k3s_land_add_attnres_rms_body<K>(partial, prefix, blocks, sw, gamma, prefix2, normed,   \
+                                     snapshot, B);                                          \
+  }
+#else
+#define K3_NBS_ENTRY(K)                                                                     \
+  extern "C" __global__ void __launch_bounds__(K3S_THREADS)                              \
+      k3h_land_add_attnres_rms_nb##K##s(                                                    \
+          const k3_land_t* __restrict__ partial, const uint16_t* __restrict__ prefix,       \
+          const uint16_t* __restrict__ blocks, const float* __restrict__ sw,                \
+          const uint16_t* __restrict__ gamma, uint16_t* __restrict__ prefix2,               \
+          uint16_t* __restrict__ normed, int nb_in, int snapshot, int B,                    \
+          const float* __restrict__ stats, int nb_stats) {                                  \
+    if (nb_in != K) return;                                                                 \
+    k3s_land_add_attnres_rms_body<K, K3_MIX_STATS_IN>(partial, prefix, blocks, sw, gamma,   \
+                                                      prefix2, normed, snapshot, B, stats, \
+                                                      nb_stats);                            \
+  }
+#endif
+
+K3_NBS_ENTRY(1)
+K3_NBS_ENTRY(2)
+K3_NBS_ENTRY(3)
+K3_NBS_ENTRY(4)
+K3_NBS_ENTRY(5)
 
 K3_NB_ENTRY(1)
 K3_NB_ENTRY(2)
