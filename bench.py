@@ -50,17 +50,23 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def make_inputs(rows: int, seed: int = 24301):
+DATA = ("synthetic: k3h_synth_normal, one xoshiro256** stream per tensor seeded "
+        "24301 ^ fnv1a64('<config>/<tensor>'), Box-Muller normals; x with 0.1% outliers x50")
+
+
+def syn(name: str, shape, mean: float = 0.0, std: float = 1.0, outlier_p: float = 0.0,
+        dtype=None):
+    """A BASELINE-config input from the seeded host generator, copied to the GPU."""
     import torch
-    g = torch.Generator(device="cuda")
-    g.manual_seed(seed)
-    x = torch.randn((rows, H), generator=g, device="cuda", dtype=torch.float32)
-    out = torch.rand((rows, H), generator=g, device="cuda") < 0.001
-    x = torch.where(out, torch.randn((rows, H), generator=g, device="cuda") * 50.0, x)
-    x = x.to(torch.bfloat16)
-    res = torch.randn((rows, H), generator=g, device="cuda", dtype=torch.float32).to(torch.bfloat16)
-    gamma = (1.0 + 0.1 * torch.randn(H, generator=g, device="cuda")).to(torch.bfloat16)
-    return x, res, gamma
+    import k3h
+    return k3h.synth_normal(name, shape, mean, std, outlier_p, 50.0,
+                            dtype or torch.bfloat16).cuda()
+
+
+def make_inputs(rows: int):
+    """Config 2: x ~N(0,1) with 0.1% outliers x50, residual ~N(0,1), gamma ~N(1,0.1)."""
+    return (syn("2/x", (rows, H), outlier_p=0.001), syn("2/residual", (rows, H)),
+            syn("2/gamma", (H,), 1.0, 0.1))
 
 
 def cpu_baseline(x, res, gamma, gpu_out, budget_s: float = 10.0) -> dict:
@@ -220,7 +226,7 @@ def bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0) -> 
     del a, b
     # config 1: K1b nb = 0 at 1024 x 7168, eps 1e-6
     B1 = 1024
-    p1, r1, g1 = bf(B1, H), bf(B1, H), bf(H, mean=1.0, std=0.1)
+    p1, r1, g1 = syn("1/x", (B1, H)), syn("1/residual", (B1, H)), syn("1/gamma", (H,), 1.0, 0.1)
     o1, n1 = torch.empty_like(p1), torch.empty_like(p1)
     sw = torch.zeros(H, dtype=torch.float32, device="cuda")
     add("residual add + RMSNorm (cfg 1)", "kern_k3_land_add_attnres_rms", f"{B1}x{H}",
@@ -249,11 +255,11 @@ def bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0) -> 
     del ro, q, sf
     # config 3: KDA span gather + output gate (24 heads x 128)
     inner = 3072
-    part = bf(T, 4 * inner)
-    cw = (torch.randn((3, 4, inner), generator=g, device="cuda") * 0.5).to(torch.bfloat16).float()
+    part = syn("3/partial", (T, 4 * inner))
+    cw = syn("3/conv_w", (3, 4, inner), std=0.5).float()
     state = torch.zeros(2 * 1628160, dtype=torch.uint8, device="cuda")
     line = torch.zeros(T, dtype=torch.int32, device="cuda")
-    wsm = torch.randn((T, 256), generator=g, device="cuda")
+    wsm = syn("3/wsm", (T, 256), dtype=torch.float32)
     sq, sk, sv = (torch.empty((T, inner), dtype=torch.bfloat16, device="cuda") for _ in range(3))
     beta = torch.empty(24 * T, dtype=torch.bfloat16, device="cuda")
     flow = torch.empty((T, 128), dtype=torch.bfloat16, device="cuda")
@@ -263,7 +269,7 @@ def bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0) -> 
         timed(lambda: ctx.span_gather(part, cw, state, line, 1628160, wsm, sq, sk, sv, beta, flow, at0, T, stream=s)),
         cpu=O and (lambda a=(h(part), h(cw), np.zeros((3, 3, inner), np.uint16), h(wsm)):
                    O.span_gather(a[0], a[1], a[2], a[3], 0, T)))
-    attn = bf(T, inner)
+    attn = syn("3/attn", (T, inner))
     gam = torch.ones(128, dtype=torch.float32, device="cuda")
     gated = torch.empty((T, inner), dtype=torch.bfloat16, device="cuda")
     add("KDA output gate (cfg 3b, eps 1e-6)", "kern_k3_kda_out_gate", f"T={T} 24x128",
@@ -273,8 +279,8 @@ def bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0) -> 
                    O.kda_out_gate(a[0], a[1], a[2], a[3], 0, T, eps=1e-6)))
     del part, sq, sk, sv, attn, gated, wsm
     # config 4: MLA prep (reference form, bf16 partial) and the RoPE + pack form
-    mp = bf(T, 5184)
-    gq, gk = bf(1536, mean=1.0, std=0.1), bf(512, mean=1.0, std=0.1)
+    mp = syn("4/partial", (T, 5184))
+    gq, gk = syn("4/gamma_q", (1536,), 1.0, 0.1), syn("4/gamma_kv", (512,), 1.0, 0.1)
     slots = torch.arange(T, dtype=torch.int64, device="cuda")
     slab = torch.empty((T // 64) * 64 * 576, dtype=torch.bfloat16, device="cuda")
     qn = torch.empty((T, 1536), dtype=torch.bfloat16, device="cuda")
@@ -285,7 +291,7 @@ def bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0) -> 
         cpu=O and (lambda a=(h(mp), h(gq), h(gk), h(slots), h(slab)):
                    O.mla_prep(a[0], a[1], a[2], a[3], a[4], 0, 64 * 576, T)))
     del mp, qn, mg
-    lat, kr, qq = bf(T, 512), bf(T, 64), bf(T, 16, 192)
+    lat, kr, qq = syn("4/latent", (T, 512)), syn("4/k_rope", (T, 64)), syn("4/q", (T, 16, 192))
     lo = torch.empty((T, 576), dtype=torch.bfloat16, device="cuda")
     qo = torch.empty_like(qq)
     add("MLA latent norm + RoPE + q pack", "k3h_mla_rope_pack", f"T={T} H=16",
@@ -295,8 +301,8 @@ def bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0) -> 
                    O.mla_rope_pack(a[0], a[1], a[2], a[3], a[4], T, 16)))
     del lat, kr, qq, lo, qo, slab
     # config 5: MoE routing + EP dispatch / finalize (top-8 of 224, EP rank 0 of 4)
-    Sx = torch.randn((T, 224), generator=g, device="cuda")
-    bias = torch.randn(224, generator=g, device="cuda") * 0.01
+    Sx = syn("5/logits", (T, 224), dtype=torch.float32)
+    bias = syn("5/bias", (224,), std=0.01, dtype=torch.float32)
     rs = torch.full((1,), 2.5, dtype=torch.bfloat16, device="cuda")
     idx = torch.empty((T, 8), dtype=torch.int32, device="cuda")
     wts = torch.empty((T, 8), dtype=torch.float32, device="cuda")
@@ -342,7 +348,7 @@ def bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0) -> 
         timed(lambda: ctx.moe_permute_mx(x8, sf8, rmap, tp, H, pq, psf, stream=s)),
         cpu=O and (lambda a=(h(x8), h(sf8), h(rmap)): O.moe_permute_mx(a[0], a[1], a[2], tpad, H)))
     del pq, psf, x8, sf8
-    fc2 = bf(tpad, H)
+    fc2 = syn("5/fc2", (tpad, H))
     out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
     add("weighted finalize (cfg 5d)", "kern_k3_moe_finalize", f"T={T} cols={H}",
         live * H * 2 + 2 * T * 8 * 4 + T * H * 2,
@@ -546,13 +552,16 @@ def bench_push_land(ctx, add, timed, bf, g, s, O=None, h=None) -> None:
                                                 sw_mlp, stats, p1, p2, prefix2, hidden, 1, stream=s)))
     part = bf(B, HH)
     pre2, nrm = torch.empty_like(part), torch.empty_like(part)
-    add("K1b nb 1 entry (manifest res_mlp)", "kern_k3_land_add_attnres_rms_nb1", f"B={B} nb=1",
-        2 * row + row + HH * 4 + HH * 2 + 2 * row,
-        timed(lambda: ctx.land_add_attnres_rms_nb(part, prefix, blocks, sw, gm, pre2, nrm, 1, 0, B,
-                                                  stream=s)),
-        cpu=O and (lambda a=(h(part), h(prefix), h(blocks), h(sw), h(gm)):
-                   O.land_add_attnres_rms(a[0], a[1], a[2], a[3], a[4], 1, 0, B)))
-    add("res_mlp nb 5 with res_in statistics (nb_stats 4)", "kern_k3_land_add_attnres_rms_nb5",
+    for k, kern in ((1, "k3h_land_add_attnres_rms_nb1s"), (4, "k3h_land_add_attnres_rms_nb4s"),
+                    (8, "kern_k3_land_add_attnres_rms_nb8")):
+        add(f"K1b nb {k} (res_mlp, typed call)", kern, f"B={B} nb={k}",
+            2 * row + k * row + HH * 4 + HH * 2 + 2 * row,
+            timed(lambda k=k: ctx.land_add_attnres_rms_nb(part, prefix, blocks, sw, gm, pre2, nrm, k,
+                                                          0, B, stream=s)),
+            "vector-split row body" if k <= 5 else "128-thread row body (reference on GB300: 155 us)",
+            cpu=O and (lambda a=(h(part), h(prefix), h(blocks), h(sw), h(gm)), k=k:
+                       O.land_add_attnres_rms(a[0], a[1], a[2], a[3], a[4], k, 0, B)))
+    add("res_mlp nb 5 with res_in statistics (nb_stats 4)", "k3h_land_add_attnres_rms_nb5s",
         f"B={B} nb=5", 2 * row + 5 * row + HH * 4 + HH * 2 + 2 * row + B * 4 * 8,
         timed(lambda: ctx.land_add_attnres_rms_nb_stats(part, prefix, blocks, sw_mlp, gm, pre2, nrm,
                                                         5, 0, B, stats, 4, stream=s)),
@@ -661,8 +670,10 @@ OP_KERNELS = {
     "weighted finalize (cfg 5d)": ["kern_k3_moe_finalize"],
     "residual push v3 (res_in, nb 0, 4 ranks)": ["kern_k3_attnres_rms_push"],
     "residual push_add2 (res_in, nb 4, 4 ranks)": ["kern_k3_attnres_rms_push"],
-    "K1b nb 1 entry (manifest res_mlp)": ["kern_k3_land_add_attnres_rms_nb1"],
-    "res_mlp nb 5 with res_in statistics (nb_stats 4)": ["kern_k3_land_add_attnres_rms_nb5"],
+    "K1b nb 1 (res_mlp, typed call)": ["k3h_land_add_attnres_rms_nb1s"],
+    "K1b nb 4 (res_mlp, typed call)": ["k3h_land_add_attnres_rms_nb4s"],
+    "K1b nb 8 (res_mlp, typed call)": ["kern_k3_land_add_attnres_rms_nb8"],
+    "res_mlp nb 5 with res_in statistics (nb_stats 4)": ["k3h_land_add_attnres_rms_nb5s"],
     "rms (l0, h 3584)": ["kern_k3_rms"],
     "land (l0, n 3584)": ["kern_k3_land"],
     "SiTU landing f32 (n 33792)": ["kern_k3_land_situ"],
@@ -785,7 +796,7 @@ def trace_table(trace_csv: str, ops_json: str) -> str:
         clean = sorted(sum(x[i] for x in runs) for i in range(5, 5 + reps))
         us = clean[len(clean) // 2]
         if r.get("bound") == "mfma":
-            rate = f" | | {r['flops'] / (us * 1e-6) / 1e12:.1f}"
+            rate = f" | | | {r['flops'] / (us * 1e-6) / 1e12:.1f}"
         else:
             gbs = r["bytes"] / (us * 1e-6) / 1e9
             rate = f" | {gbs:.1f} | {100 * gbs / PEAK_GBS:.1f} | "
@@ -987,7 +998,7 @@ def main() -> int:
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1,
         "steps": a.steps, "warmup": a.warmup, "warmup_launches": n_warm, "ms_per_step": round(ms, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic (torch randn from seed 24301; 0.1% outliers x50)",
+        "data": DATA,
         "config": {"workload": "fused residual add + RMSNorm + MXFP8 (BASELINE config 2)",
                    "tokens": rows, "hidden": H, "eps": 1e-6, "block": 32,
                    "payload": "e4m3 (OCP)", "scale": "E8M0"},

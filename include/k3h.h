@@ -369,6 +369,16 @@ K3H_API int k3h_moe_fc2(k3h_ctx_t ctx, void* stream, const void* w2t, const void
                         const int* num_non_exiting, const int* total_padded, const int* cta_batch,
                         const int* cta_limit, int max_tiles, int E, int inter, int cols);
 
+/* k3h_synth_normal: measurement support (host code, no GPU): the synthetic
+ * inputs of the benchmark configurations.  n values of mean + std * N(0,1) from
+ * the tensor's own xoshiro256** stream (splitmix64-seeded with 24301 ^
+ * fnv1a64(name), Box-Muller in double, rounded to f32, then to bf16 when
+ * bf16_out); with outlier_p > 0 each element is replaced, with probability
+ * outlier_p, by outlier_x * N(0,1) from two more streams (name + "#bernoulli"
+ * selects, name + "#outlier" draws).  out: n bf16 (uint16) or f32 values. */
+K3H_API int k3h_synth_normal(const char* name, size_t n, float mean, float std_dev, float outlier_p,
+                             float outlier_x, int bf16_out, void* out);
+
 /* ---- measurement support --------------------------------------------------
  * k3h_stream_copy: dst[i] = src[i] for n16 16-byte vectors with non-temporal
  * loads and stores, one vector per thread (module k3h_fused).  No reference

@@ -113,7 +113,7 @@ DEVICE_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
-HOST_SOURCES = ["k3h_module.cpp", "k3h_ops_residual.cpp", "k3h_ops_push.cpp", "k3h_ops_land.cpp", "k3h_ops_gemm.cpp", "k3h_ops_quant.cpp", "k3h_ops_moe.cpp", "k3h_ops_kda.cpp", "k3h_ops_mla.cpp"]
+HOST_SOURCES = ["k3h_module.cpp", "k3h_ops_residual.cpp", "k3h_ops_push.cpp", "k3h_ops_land.cpp", "k3h_ops_gemm.cpp", "k3h_ops_quant.cpp", "k3h_ops_moe.cpp", "k3h_ops_kda.cpp", "k3h_ops_mla.cpp", "k3h_synth.cpp"]
 # host sources that carry device data (compiled as HIP for gfx950 into the library)
 HOST_HIP_SOURCES = ["k3h_noalloc.hip"]
 

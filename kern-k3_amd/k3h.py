@@ -58,6 +58,7 @@ _SIGS: dict[str, list] = {
     "k3h_module_unload": [_P],
     "k3h_runtime_version": [ctypes.POINTER(_I)],
     "k3h_ctx_create": [ctypes.c_char_p, ctypes.POINTER(_P)],
+    "k3h_synth_normal": [ctypes.c_char_p, ctypes.c_size_t, _F, _F, _F, _F, _I, _P],
     "k3h_ctx_destroy": [_P],
     "k3h_ctx_function": [_P, ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_P)],
     "k3h_land_add_attnres_rms": [_P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F],
@@ -119,6 +120,27 @@ def lib() -> ctypes.CDLL:
         L.k3h_error_string.restype = ctypes.c_char_p
         _lib = L
     return _lib
+
+
+def synth_normal(name: str, shape, mean: float = 0.0, std: float = 1.0, outlier_p: float = 0.0,
+                 outlier_x: float = 50.0, dtype=torch.bfloat16) -> torch.Tensor:
+    """Seeded synthetic input on the host (k3h_synth_normal): the tensor's own
+    xoshiro256** stream, seed 24301 ^ fnv1a64(name), Box-Muller normals; bf16 or f32."""
+    n = 1
+    for d in shape:
+        n *= int(d)
+    if dtype == torch.bfloat16:
+        out = torch.empty(n, dtype=torch.int16)
+    elif dtype == torch.float32:
+        out = torch.empty(n, dtype=torch.float32)
+    else:
+        raise ValueError("synth_normal: bfloat16 or float32")
+    _check(lib().k3h_synth_normal(name.encode(), n, mean, std, outlier_p, outlier_x,
+                                  int(dtype == torch.bfloat16), out.data_ptr() if n else None),
+           "synth_normal")
+    if dtype == torch.bfloat16:
+        out = out.view(torch.bfloat16)
+    return out.view(*shape)
 
 
 def error_string(code: int) -> str:
