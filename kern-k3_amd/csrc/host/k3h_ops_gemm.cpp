@@ -9,12 +9,13 @@
 // weight arguments are this build's tiled layouts (k3h_moe_w_tile /
 // k3h_moe_sf_tile), not the reference GEMMs' shuffled ones.
 #include <algorithm>
+#include <atomic>
 
 #include "k3h_internal.h"
 
 namespace {
-constexpr uint32_t kBlock = 256;
-constexpr int kTileN = 256, kStepK = 128;
+constexpr uint32_t kBlock = 256, kBlockWide = 512;
+constexpr int kTileN = 256, kTileNWide = 512, kStepK = 128;
 
 // The kernels keep the tile's A scales (K / 32 bytes per row) in LDS: entries
 // without a suffix take K <= 3584, the "_w" entries K <= 7168.
@@ -47,6 +48,26 @@ uint32_t gemm_grid_rows(int max_tiles, int nc) {
     need = std::max<int64_t>(need, 8 * k3h_cdiv(max_tiles, xt) * k3h_cdiv(nc, xc));
   }
   return (uint32_t)k3h_cdiv(need, nc);
+}
+
+// Compute units of the device `stream` runs on (the current device for the null
+// stream), cached per device.
+int stream_cus(void* stream, int* cus) {
+  static std::atomic<int> cache[64];
+  int dev = -1;
+  hipError_t e = stream ? hipStreamGetDevice(static_cast<hipStream_t>(stream), &dev)
+                        : hipGetDevice(&dev);
+  if (e != hipSuccess) return k3h_hip(e);
+  if (dev < 0 || dev >= 64) return K3H_EINVAL;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return k3h_hip(e);
+    if (n <= 0) return K3H_EINVAL;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  *cus = n;
+  return K3H_OK;
 }
 
 bool gemm_ptrs_ok(const void* a, const void* a_sf, const int* a_rows, const void* wt,
@@ -117,6 +138,19 @@ K3H_API int k3h_moe_gemm_mx(k3h_ctx_t ctx, void* stream, int epilogue, const voi
       return K3H_EINVAL;
   }
   if (max_tiles == 0) return K3H_OK;
+  // f32 / bf16 epilogues on 512-column items: persistent 8-wave workgroups
+  // (kern_k3h_moe_gemm2_*, one per CU, grid a multiple of the 8 XCDs) where the
+  // shape allows them; else, and for the SiTU-GLU + MXFP8 epilogue, 256-column
+  // items on 4-wave workgroups (two per CU).
+  if (epilogue != K3H_GEMM_SITU_MX && N % kTileNWide == 0 && K >= 2 * kStepK &&
+      K <= kMaxKNarrow && k3h_aligned(out, 16)) {
+    int cus = 0;
+    if (const int rc = stream_cus(stream, &cus)) return rc;
+    const uint32_t grid = (uint32_t)std::max(8, cus / 8 * 8);
+    return k3h_run(ctx, "k3h_moe_gemm",
+                   epilogue == K3H_GEMM_F32 ? "kern_k3h_moe_gemm2_f32" : "kern_k3h_moe_gemm2_bf16",
+                   grid, 1, 1, kBlockWide, stream, args);
+  }
   const uint32_t rows = gemm_grid_rows(max_tiles, N / kTileN);
   if (rows > 65535u) return K3H_EINVAL;
   return k3h_run(ctx, "k3h_moe_gemm", entry, (uint32_t)(N / kTileN), rows, 1, kBlock, stream, args);

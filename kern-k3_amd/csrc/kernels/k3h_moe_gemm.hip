@@ -565,3 +565,6 @@ K3_DEV void k3g_gemm_situ_mx(K3G_PARAMS, uint8_t* __restrict__ out_q, uint8_t* _
   }
 K3G_ENTRIES(, 112)
 K3G_ENTRIES(_w, 224)
+
+#include "k3_gemm_wide.h"
+K3W_ENTRIES

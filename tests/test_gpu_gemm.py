@@ -117,8 +117,15 @@ def _check_acc(got, q, sf, rows, w, wsf, cta, nt, E, N, K):
     return ref, mag, live
 
 
+# N % 512 == 0 and 256 <= K <= 3584 run the 512-column 8-wave entries
+# (kern_k3h_moe_gemm2_*_r{(K/128 - 2) % 3}: K 256 / 384 / 512 are their shortest
+# pipelines of each tail class, 3072 and 3584 the fc2 / fc1 depths); the others
+# the 256-column entries (K > 3584: the _w entries).
 @pytest.mark.parametrize("E,N,K,gather", [(4, 512, 1024, True), (3, 256, 3584, False),
-                                          (2, 768, 256, True), (2, 256, 7168, True)])
+                                          (2, 768, 256, True), (2, 256, 7168, True),
+                                          (2, 512, 3584, True), (3, 1024, 3072, False),
+                                          (2, 512, 256, True), (2, 512, 384, False),
+                                          (2, 1536, 512, True)])
 def test_gemm_f32_accumulators(ctx, E, N, K, gather):
     _case(f"gemm f32 E={E} N={N} K={K} gather={gather}")
     rows_src = 700
@@ -137,10 +144,10 @@ def test_gemm_f32_accumulators(ctx, E, N, K, gather):
     _check_acc(got, qa, sfa, rows, w, wsf, cta, nt, E, N, K)
 
 
-def test_gemm_bf16(ctx):
-    _case("gemm bf16 (fc2 form)")
-    E, N, K = 3, 512, 1024
-    g, q, sf, w, wsf = _inputs(7300, 512, E, N, K)
+@pytest.mark.parametrize("E,N,K", [(3, 512, 1024), (3, 1024, 3072), (3, 256, 1024)])
+def test_gemm_bf16(ctx, E, N, K):
+    _case(f"gemm bf16 (fc2 form) E={E} N={N} K={K}")
+    g, q, sf, w, wsf = _inputs(7300 + N + K, 512, E, N, K)
     cta = np.array([2, 0, 1, 1], np.int32)
     nt = max_tiles = 4
     wt, st = _tiled(ctx, w, wsf, E, N, K, 0)
@@ -167,7 +174,8 @@ def _logical_to_raw(c, N):
 
 
 @pytest.mark.parametrize("E,inter,K,ab", [(4, 256, 1024, (4.0, 25.0)), (2, 128, 3584, (4.0, 25.0)),
-                                          (3, 384, 512, (3.0, 20.0))])
+                                          (3, 384, 512, (3.0, 20.0)), (2, 256, 3584, (4.0, 25.0)),
+                                          (2, 512, 384, (3.0, 20.0))])
 def test_gemm_situ_mx(ctx, E, inter, K, ab):
     _case(f"gemm situ_mx (fc1 form) E={E} inter={inter} K={K} alpha,beta={ab}")
     N = 2 * inter
@@ -220,3 +228,54 @@ def test_gemm_rejects_bad_shapes(ctx):
     big = torch.zeros(1 << 21, dtype=torch.uint8, device="cuda")
     with pytest.raises(ValueError):  # K above the scale table's 7168
         ctx.moe_gemm_mx(ctx.GEMM_F32, big, big, None, big, big, i, i, 1, 1, 256, 7296, f)
+
+
+def _grid_rows(max_tiles, nc):
+    """Rows of the 4-wave kernels' grid (k3h_moe_gemm_mx's split coverage)."""
+    need = max(8 * -(-max_tiles // (8 // xc)) * -(-nc // xc) for xc in (1, 2, 4, 8))
+    return -(-need // nc)
+
+
+@pytest.mark.parametrize("K", [256, 384, 1536])
+def test_wide_items_match_4wave(ctx, K):
+    """The persistent 512-column entries (kern_k3h_moe_gemm2_f32 / _bf16, which the
+    typed calls take for N % 512 == 0 and K <= 3584) against the 4-wave entries
+    launched directly, bit for bit, at a size where every workgroup runs several
+    items back to back (the step pipeline crossing items) and some tiles have an
+    out-of-range expert or lie past the live count.  The 4-wave entries are pinned
+    against the oracle by the tests above."""
+    import ctypes
+    import k3h
+    E, N, live, max_tiles = 6, 1024, 1100, 1120
+    _case(f"wide vs 4-wave E={E} N={N} K={K} tiles={live}")
+    g = rng(7700 + K)
+    rows_src = 4096
+    q = g.integers(0, 256, (rows_src, K), dtype=np.uint8)
+    q[(q & 0x7f) == 0x7f] = 0x3c  # no NaN codes
+    sf = g.integers(120, 130, (rows_src, K // 32)).astype(np.uint8)
+    w = g.integers(0, 256, (E, N, K // 2), dtype=np.uint8)
+    wsf = g.integers(118, 134, (E, N, K // 32)).astype(np.uint8)
+    cta = np.sort(g.integers(0, E, max_tiles)).astype(np.int32)
+    cta[g.integers(0, live, 40)] = E  # out-of-range experts (skipped items)
+    rows = g.integers(-1, rows_src, max_tiles * 128).astype(np.int32)  # -1: padding rows
+    wt, st = _tiled(ctx, w, wsf, E, N, K, 0)
+    dq, dsf, dr, dcta = to_dev(q), to_dev(sf), to_dev(rows), to_dev(cta)
+    nt = to_dev(np.array([live], np.int32))
+    for ep, dt, fill, entry in ((ctx.GEMM_F32, torch.float32, float("nan"), "kern_k3h_moe_gemm_f32"),
+                                (ctx.GEMM_BF16, torch.bfloat16, 0.0, "kern_k3h_moe_gemm_bf16")):
+        got = torch.full((max_tiles * 128, N), fill, dtype=dt, device="cuda")
+        ctx.moe_gemm_mx(ep, dq, dsf, dr, wt, st, nt, dcta, max_tiles, E, N, K, got)
+        ref = torch.full_like(got, fill)
+        args = k3h.pack_args(["buffer"] * 7 + ["i32"] * 4 + ["buffer"],
+                             [dq, dsf, dr, wt, st, nt, dcta, E, N, K, max_tiles, ref])
+        fn = ctx.function("k3h_moe_gemm", entry)
+        grid = (ctypes.c_uint32 * 3)(N // 256, _grid_rows(max_tiles, N // 256), 1)
+        block = (ctypes.c_uint32 * 3)(256, 1, 1)
+        cbuf = ctypes.create_string_buffer(args, len(args))
+        k3h._check(ctx.L.k3h_launch(fn, grid, block, 0, None, ctypes.cast(cbuf, ctypes.c_void_p),
+                                    len(args)), entry)
+        torch.cuda.synchronize()
+        a, b = from_dev(got), from_dev(ref)
+        same = (a.view(np.uint8) == b.view(np.uint8)).all()
+        print(f"  {entry}: identical = {same}", flush=True)
+        assert same
