@@ -641,7 +641,7 @@ def bench_gemm(ctx, add_flop, timed, g, s, rmap, cta_batch, num_tiles, tpad, T, 
                                            cta_batch, max_tiles, E, 2 * INTER, KL, o1, o1sf, alpha,
                                            beta, stream=s)),
              "e4m3 x e2m1 MFMA; gathers rows through route_map")
-    add_flop("MoE fc2 (MX GEMM, bf16 out)", "kern_k3h_moe_gemm_bf16",
+    add_flop("MoE fc2 (MX GEMM, bf16 out)", "kern_k3h_moe_gemm2_bf16",
              f"{tpad} rows x {INTER} -> {COLS}, E={E}", 2 * tpad * INTER * COLS,
              E * COLS * (INTER // 2 + INTER // 32) + tpad * (INTER + INTER // 32) + tpad * COLS * 2,
              timed(lambda: ctx.moe_gemm_mx(ctx.GEMM_BF16, o1, o1sf, None, w2, s2, num_tiles,
@@ -681,7 +681,7 @@ OP_KERNELS = {
     "SiTU landing bf16 (l0, n 33792)": ["kern_k3_situ_bf16"],
     "SiTU landing + latent rms (fused)": ["kern_k3_situ_rms_bf16"],
     "MoE fc1 (MX GEMM + SiTU-GLU + MXFP8)": ["kern_k3h_moe_gemm_situ_mx"],
-    "MoE fc2 (MX GEMM, bf16 out)": ["kern_k3h_moe_gemm_bf16"],
+    "MoE fc2 (MX GEMM, bf16 out)": ["kern_k3h_moe_gemm2_bf16"],
 }
 
 

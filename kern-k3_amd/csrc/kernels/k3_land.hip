@@ -107,12 +107,24 @@ K3_DEV float k3_bfly32_tree(const float* w, int nw) {
 template <int NK>
 K3_DEV void k3_rms_row_wave(const uint16_t* __restrict__ xr, const uint16_t* __restrict__ gamma,
                             uint16_t* __restrict__ orow, int nvec, int h, int lane) {
-  k3_u4 xv[NK];
+  // NK <= 8: every load (the row, then gamma) is issued before the reduction, so
+  // that no load waits behind a store (the vector memory counter retires in
+  // order); wider rows load gamma beside the stores (register budget)
+  constexpr bool PRE = NK <= 8;
+  k3_u4 xv[NK], gv[PRE ? NK : 1];
 #pragma unroll
   for (int k = 0; k < NK; ++k) {
     if (k * 64 >= nvec) break;
     const int u = min(lane + 64 * k, nvec - 1);
     xv[k] = k3_ld16_nt(xr + 8 * u);
+  }
+  if constexpr (PRE) {
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+      if (k * 64 >= nvec) break;
+      const int u = min(lane + 64 * k, nvec - 1);
+      gv[k] = k3_ld16(gamma + 8 * u);
+    }
   }
   float wsum[2 * NK];
 #pragma unroll
@@ -138,7 +150,7 @@ K3_DEV void k3_rms_row_wave(const uint16_t* __restrict__ xr, const uint16_t* __r
     if (k * 64 >= nvec) break;
     const int u = lane + 64 * k;
     if (u < nvec) {
-      const k3_u4 g = k3_ld16(gamma + 8 * u);
+      const k3_u4 g = PRE ? gv[PRE ? k : 0] : k3_ld16(gamma + 8 * u);
       k3_u4 o;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
@@ -211,7 +223,11 @@ extern "C" __global__ void __launch_bounds__(1024) kern_k3_rms(
     // reference's 1024-thread block, the launch geometry of the manifest
     const int b = blockIdx.x * (int)(blockDim.x >> 6) + (int)(threadIdx.x >> 6);
     if (b >= B) return;
-    k3_rms_row_wave<16>(x + (size_t)b * h, gamma, o + (size_t)b * h, h >> 3, h, threadIdx.x & 63);
+    const int nvec = h >> 3;
+    if (nvec <= 512)  // h <= 4096: up to 8 vectors per lane
+      k3_rms_row_wave<8>(x + (size_t)b * h, gamma, o + (size_t)b * h, nvec, h, threadIdx.x & 63);
+    else
+      k3_rms_row_wave<16>(x + (size_t)b * h, gamma, o + (size_t)b * h, nvec, h, threadIdx.x & 63);
     return;
   }
   const int b = blockIdx.x;

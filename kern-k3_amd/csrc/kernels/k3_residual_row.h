@@ -447,6 +447,45 @@ K3_DEV k3_u4 k3_add_land(k3_u4 prefix, k3_u4 landed) {
   return o;
 }
 
+// K1b row without candidates (nb == 0): every load first (the landing operands
+// and gamma), the reduction, then the prefix2 and normed stores, so that no load
+// waits behind a store (the vector memory counter retires in order).  Same
+// arithmetic as the general body at nb == 0.
+K3_DEV void k3_land_add_rms_nb0(const k3_land_t* __restrict__ partial,
+                                const uint16_t* __restrict__ prefix,
+                                const uint16_t* __restrict__ gamma,
+                                uint16_t* __restrict__ prefix2, uint16_t* __restrict__ normed,
+                                int snapshot, int b, int t, float eps) {
+  __shared__ float s_red0[K3_NHW];
+  k3_u4 pv[K3_KVPT], pr[K3_KVPT], g[K3_KVPT];
+#pragma unroll
+  for (int v = 0; v < K3_KVPT; ++v) pv[v] = k3_load_land(partial, (size_t)b * K3_H + k3_vec_off(t, v));
+  if (!snapshot) {
+#pragma unroll
+    for (int v = 0; v < K3_KVPT; ++v) pr[v] = k3_ld16_nt(prefix + (size_t)b * K3_H + k3_vec_off(t, v));
+  }
+#pragma unroll
+  for (int v = 0; v < K3_KVPT; ++v) g[v] = k3_ld16(gamma + k3_vec_off(t, v));
+  if (!snapshot) {
+#pragma unroll
+    for (int v = 0; v < K3_KVPT; ++v) pv[v] = k3_add_land(pr[v], pv[v]);
+  }
+  const float tot = k3_block_sum128(k3_row_sumsq(pv), s_red0, t);
+  const float r = k3_row_rscale(tot, eps);
+#pragma unroll
+  for (int v = 0; v < K3_KVPT; ++v) k3_st16_nt(prefix2 + (size_t)b * K3_H + k3_vec_off(t, v), pv[v]);
+#pragma unroll
+  for (int v = 0; v < K3_KVPT; ++v) {
+    k3_u4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t y = k3_pack_bf2(k3_bf_lo(pv[v][j]) * r, k3_bf_hi(pv[v][j]) * r);
+      o[j] = k3_mul_bf2(y, g[v][j]);
+    }
+    k3_st16_nt(normed + (size_t)b * K3_H + k3_vec_off(t, v), o);
+  }
+}
+
 // K1b entry body shared by the run-time-nb entry and the per-nb entries.  With
 // MODE = K3_MIX_STATS_IN the first nb_stats candidates' statistics come from
 // stats[b] ([B, K3_NB_MAX, 2], written by the push-stats entry of res_in).
@@ -463,6 +502,10 @@ K3_DEV void k3_land_add_attnres_rms_body(const k3_land_t* __restrict__ partial,
   const int b = blockIdx.x;
   if (b >= B) return;
   const int t = threadIdx.x;
+  if (NBC <= 0 && nb == 0) {
+    k3_land_add_rms_nb0(partial, prefix, gamma, prefix2, normed, snapshot, b, t, K3_EPS);
+    return;
+  }
   // all row loads first, then the landing adds and the prefix2 stores (a store
   // between two loads would make the second load's wait cover the store too)
   k3_u4 pv[K3_KVPT], pr[K3_KVPT];
