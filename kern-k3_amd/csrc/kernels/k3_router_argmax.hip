@@ -30,6 +30,24 @@
 #define RSLOTS ((EXPERTS + 63) / 64)  // 4 slots per lane
 static_assert(TOPK >= 1 && TOPK <= 32 && (TOPK & (TOPK - 1)) == 0, "TOPK: power of two <= 32");
 
+// Largest value over the wave, on every lane (DPP steps fused with the max:
+// quad swaps, half-row and row mirrors, then the row broadcasts 15 and 31).
+K3_DEV uint32_t k3_router_wave_max(uint32_t v) {
+  uint32_t o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, K3_DPP_QP_1032, 0xf, 0xf, true);
+  v = v > o ? v : o;
+  o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, K3_DPP_QP_2301, 0xf, 0xf, true);
+  v = v > o ? v : o;
+  o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, K3_DPP_ROW_HALF_MIRROR, 0xf, 0xf, true);
+  v = v > o ? v : o;
+  o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, K3_DPP_ROW_MIRROR, 0xf, 0xf, true);
+  v = v > o ? v : o;
+  o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, K3_DPP_ROW_BCAST15, 0xa, 0xf, false);
+  v = v > o ? v : o;
+  o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, K3_DPP_ROW_BCAST31, 0xc, 0xf, false);
+  v = v > o ? v : o;
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
 // Row b on one full wave (expert e = lane + 64 j in slot j of lane `lane`).
 K3_DEV void k3_router_row(const float* __restrict__ S, const float* __restrict__ bias,
                           const uint16_t* __restrict__ rs, int* __restrict__ idx,
@@ -56,33 +74,54 @@ K3_DEV void k3_router_row(const float* __restrict__ S, const float* __restrict__
     key[j] = ok ? k3_ord_f32(sig[j] + bv_[j]) : 0u;
   }
 
-  // A pick is a DPP wave max of the keys (uniform) and a ballot per slot for the
-  // lanes holding it: slots are scanned from the top so the lowest slot, and in
-  // it the lowest lane, i.e. the smallest expert id, wins.  (Keeping a per-lane
-  // best and breaking cross-lane ties by a second wave min only when a ballot
-  // has more than one lane measured no faster: 16.0 against 15.8 us.)
-  int my_idx = 0;
-  float my_sig = 0.0f;
+  // Each lane keeps its four (key, slot) sorted, largest key first and ties to
+  // the smaller slot, so a pick is a DPP wave max over the lanes' heads and one
+  // ballot; the winner's head advances.  The smallest expert id among the keys
+  // equal to the maximum is always some lane's head, so when several heads hold
+  // it (rare) a second wave max over 255 - (64 slot + lane) of those lanes picks
+  // it, as the reference's order does.  Lane r < TOPK notes pick r's lane and
+  // slot; the sigmoids are fetched once after the picks.
+  uint32_t hk[RSLOTS];
+  int jj[RSLOTS];
+#pragma unroll
+  for (int j = 0; j < RSLOTS; ++j) { hk[j] = key[j]; jj[j] = j; }
+  auto cswap = [&](int x, int y) {  // order positions x < y
+    const bool sw = hk[x] < hk[y] || (hk[x] == hk[y] && jj[x] > jj[y]);
+    const uint32_t kx = hk[x], ky = hk[y];
+    const int jx = jj[x], jy = jj[y];
+    hk[x] = sw ? ky : kx; hk[y] = sw ? kx : ky;
+    jj[x] = sw ? jy : jx; jj[y] = sw ? jx : jy;
+  };
+  static_assert(RSLOTS == 4, "four slots per lane");
+  cswap(0, 1); cswap(2, 3); cswap(0, 2); cswap(1, 3); cswap(1, 2);
+
+  int my_lw = 0, my_jw = 0;
   for (int r = 0; r < TOPK; ++r) {
-    uint32_t m = key[0];
-#pragma unroll
-    for (int j = 1; j < RSLOTS; ++j) m = m > key[j] ? m : key[j];
-    m = k3_wave_max_u32_uniform(m);
-    int jw = 0, lw = 0;
-#pragma unroll
-    for (int j = RSLOTS - 1; j >= 0; --j) {
-      const unsigned long long mk = __ballot(key[j] == m);
-      if (mk) { jw = j; lw = __builtin_ctzll(mk); }
+    const uint32_t m = k3_router_wave_max(hk[0]);
+    const unsigned long long mk = __ballot(hk[0] == m);
+    int lw;
+    if (__builtin_popcountll(mk) == 1) {
+      lw = __builtin_ctzll(mk);
+    } else {
+      const uint32_t cand = hk[0] == m ? 255u - (uint32_t)(64 * jj[0] + lane) : 0u;
+      lw = (int)((255u - k3_router_wave_max(cand)) & 63u);
     }
-    float sv = sig[0];
+    const int jw = __builtin_amdgcn_readlane(jj[0], lw);
+    if (lane == lw) {
 #pragma unroll
-    for (int j = 1; j < RSLOTS; ++j) sv = jw == j ? sig[j] : sv;
-    const float sw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv), lw));
-#pragma unroll
-    for (int j = 0; j < RSLOTS; ++j)
-      if (j == jw && lane == lw) key[j] = 0u;
-    if (lane == r) { my_idx = 64 * jw + lw; my_sig = sw; }
+      for (int j = 0; j + 1 < RSLOTS; ++j) { hk[j] = hk[j + 1]; jj[j] = jj[j + 1]; }
+      hk[RSLOTS - 1] = 0u;
+    }
+    if (lane == r) { my_lw = lw; my_jw = jw; }
   }
+  // pick r's sigmoid: slot my_jw of lane my_lw
+  float my_sig = 0.0f;
+#pragma unroll
+  for (int j = 0; j < RSLOTS; ++j) {
+    const float t = __shfl(sig[j], my_lw, 64);
+    my_sig = my_jw == j ? t : my_sig;
+  }
+  const int my_idx = 64 * my_jw + my_lw;
 
   // renormalise over the TOPK pick lanes: butterfly TOPK/2 .. 1, identical bits on every lane
   float den = my_sig;
