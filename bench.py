@@ -546,7 +546,7 @@ def bench_push_land(ctx, add, timed, bf, g, s, O=None, h=None) -> None:
     p1, p2, prefix2 = bf(B, HH), bf(B, HH), bf(B, HH)
     hidden = torch.empty_like(p1)
     stats = torch.empty((B, 8, 2), dtype=torch.float32, device="cuda")
-    add("residual push_add2 (res_in, nb 4, 4 ranks)", "kern_k3_attnres_rms_push",
+    add("residual push_add2 (res_in, nb 4, 4 ranks)", "k3h_attnres_rms_push_nb4s",
         f"B={B} nb={nb} two=1", 3 * row + nb * row + 2 * HH * 4 + HH * 2 + row + row + 4 * row + B * nb * 8,
         timed(lambda: ctx.attnres_rms_push_add2(blocks, sw, gm, normed[0], peer, nb, 1, B, 0, 4,
                                                 sw_mlp, stats, p1, p2, prefix2, hidden, 1, stream=s)))
@@ -669,7 +669,7 @@ OP_KERNELS = {
     "MXFP8 permute (cfg 5c)": ["k3h_moe_permute_mx"],
     "weighted finalize (cfg 5d)": ["kern_k3_moe_finalize"],
     "residual push v3 (res_in, nb 0, 4 ranks)": ["kern_k3_attnres_rms_push"],
-    "residual push_add2 (res_in, nb 4, 4 ranks)": ["kern_k3_attnres_rms_push"],
+    "residual push_add2 (res_in, nb 4, 4 ranks)": ["k3h_attnres_rms_push_nb4s"],
     "K1b nb 1 (res_mlp, typed call)": ["k3h_land_add_attnres_rms_nb1s"],
     "K1b nb 4 (res_mlp, typed call)": ["k3h_land_add_attnres_rms_nb4s"],
     "K1b nb 8 (res_mlp, typed call)": ["kern_k3_land_add_attnres_rms_nb8"],

@@ -28,6 +28,18 @@ int check_push(const void* blocks, const float* sw, const void* gamma, const voi
   return K3H_OK;
 }
 
+// 1 <= nb <= kSplitNbMax: the module's 256-thread vector-split entry for that nb
+// (same parameter list and outputs); otherwise the 128-thread entry.
+struct PushEntry {
+  std::string name;
+  uint32_t threads;
+};
+PushEntry push_entry(int nb) {
+  if (nb >= 1 && nb <= kSplitNbMax)
+    return {"k3h_attnres_rms_push_nb" + std::to_string(nb) + "s", kSplitThreads};
+  return {"kern_k3_attnres_rms_push", kResThreads};
+}
+
 void push_common(K3hArgs& a, void* blocks, const float* sw, const void* gamma, void* normed_all,
                  const unsigned long long* dst_peer, int nb, int snapshot, int B, int rank,
                  int nranks) {
@@ -51,8 +63,9 @@ K3H_API int k3h_attnres_rms_push(k3h_ctx_t ctx, void* stream, int version, const
   K3hArgs a;
   a.ptr(prefix);
   push_common(a, blocks, sw, gamma, normed_all, dst_peer, nb, snapshot, B, rank, nranks);
-  return k3h_run(ctx, version == 1 ? "k3_residual_push" : "k3_residual_push_v3",
-                 "kern_k3_attnres_rms_push", (uint32_t)B, 1, 1, kResThreads, stream, a);
+  const PushEntry e = push_entry(nb);
+  return k3h_run(ctx, version == 1 ? "k3_residual_push" : "k3_residual_push_v3", e.name.c_str(),
+                 (uint32_t)B, 1, 1, e.threads, stream, a);
 }
 
 K3H_API int k3h_attnres_rms_push_stats(k3h_ctx_t ctx, void* stream, const void* prefix,
@@ -70,8 +83,9 @@ K3H_API int k3h_attnres_rms_push_stats(k3h_ctx_t ctx, void* stream, const void* 
   a.ptr(prefix);
   push_common(a, blocks, sw, gamma, normed_all, dst_peer, nb, snapshot, B, rank, nranks);
   a.ptr(sw_mlp).ptr(stats);
-  return k3h_run(ctx, "k3_residual_push_stats", "kern_k3_attnres_rms_push", (uint32_t)B, 1, 1,
-                 kResThreads, stream, a);
+  const PushEntry e = push_entry(nb);
+  return k3h_run(ctx, "k3_residual_push_stats", e.name.c_str(), (uint32_t)B, 1, 1, e.threads,
+                 stream, a);
 }
 
 K3H_API int k3h_attnres_rms_push_add2(k3h_ctx_t ctx, void* stream, void* blocks, const float* sw,
@@ -90,8 +104,9 @@ K3H_API int k3h_attnres_rms_push_add2(k3h_ctx_t ctx, void* stream, void* blocks,
   K3hArgs a;
   push_common(a, blocks, sw, gamma, normed_all, dst_peer, nb, snapshot, B, rank, nranks);
   a.ptr(sw_mlp).ptr(stats).ptr(p1).ptr(p2).ptr(prefix2).ptr(hidden).i32(two);
-  return k3h_run(ctx, "k3_residual_push_add2", "kern_k3_attnres_rms_push", (uint32_t)B, 1, 1,
-                 kResThreads, stream, a);
+  const PushEntry e = push_entry(nb);
+  return k3h_run(ctx, "k3_residual_push_add2", e.name.c_str(), (uint32_t)B, 1, 1, e.threads,
+                 stream, a);
 }
 
 K3H_API int k3h_land_add_attnres_rms_nb_stats(k3h_ctx_t ctx, void* stream, const void* partial,

@@ -15,6 +15,11 @@
 //
 // grid (B, 1, 1), block (128, 1, 1) (manifest ceil_div(tokens, 4) rows per rank).
 //
+// Typed-call entries k3h_attnres_rms_push_nb{K}s (K = 1..5, nb == K; same
+// parameter list as the module's entry, block 256): the vector-split row body
+// (k3_residual_split.h), every candidate held on chip from pass 1 to pass 2,
+// the same bits.
+//
 // Row b of this rank lands at row rank * B + b of every rank's normed_all: the
 // local copy through `normed_all`, the others through dst_peer[q] (q < nranks,
 // q != rank; nranks is capped at 8), each a device address of rank q's
@@ -27,6 +32,7 @@
 // is copied to blocks[b, nb] first.  No fence: the stores are released by the
 // arrival barrier, a later launch on the same stream.
 #include "k3_residual_row.h"
+#include "k3_residual_split.h"
 
 #ifndef K3_PUSH
 #define K3_PUSH 1
@@ -116,3 +122,123 @@ extern "C" __global__ void __launch_bounds__(K3_RES_THREADS) kern_k3_attnres_rms
                             K3_PUSH_EPS, t);
 #endif
 }
+
+// ---------------------------------------------------------------- split form
+template <int NB>
+K3_DEV void k3s_push_body(
+#if K3_PUSH != 3
+    const uint16_t* __restrict__ prefix,
+#endif
+    uint16_t* __restrict__ blocks, const float* __restrict__ sw,
+    const uint16_t* __restrict__ gamma, uint16_t* __restrict__ normed_all,
+    const unsigned long long* __restrict__ dst_peer, int snapshot, int B, int rank, int nranks
+#if K3_PUSH >= 2
+    , const float* __restrict__ sw_mlp, float* __restrict__ stats
+#endif
+#if K3_PUSH == 3
+    , const uint16_t* __restrict__ p1, const uint16_t* __restrict__ p2,
+    const uint16_t* __restrict__ prefix2, uint16_t* __restrict__ hidden, int two
+#endif
+) {
+  const int b = blockIdx.x;
+  if (b >= B) return;
+  const K3sLane L = k3s_lane();
+  const int nr = nranks < K3_MAX_RANKS ? nranks : K3_MAX_RANKS;
+  const long long dst_off = ((long long)rank * B + b) * K3_H;
+  const size_t row = (size_t)b * K3_H;
+  // every load of the row (the prefix or its land_add2 operands, the candidates)
+  // goes out before the first store
+  k3_u4 pv[K3S_SLOTS];
+#if K3_PUSH == 3
+  k3_u4 a[K3S_SLOTS], e[K3S_SLOTS];
+#pragma unroll
+  for (int s = 0; s < K3S_SLOTS; ++s) {
+    a[s] = k3_ld16_nt(p1 + row + L.off(s));
+    pv[s] = k3_ld16_nt(prefix2 + row + L.off(s));
+  }
+  if (two) {
+#pragma unroll
+    for (int s = 0; s < K3S_SLOTS; ++s) e[s] = k3_ld16_nt(p2 + row + L.off(s));
+  }
+#else
+#pragma unroll
+  for (int s = 0; s < K3S_SLOTS; ++s) pv[s] = k3_ld16_nt(prefix + row + L.off(s));
+#endif
+  k3_u4 xc[NB][K3S_SLOTS];
+  k3s_load_candidates<NB>(xc, blocks + (size_t)b * K3_NB_MAX * K3_H, L);
+#if K3_PUSH == 3
+  // hidden = bf16(f32(prefix2) + f32(p1) [+ f32(p2)]), left to right, one rounding
+#pragma unroll
+  for (int s = 0; s < K3S_SLOTS; ++s) {
+    k3_u4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float x = k3_bf_lo(pv[s][j]) + k3_bf_lo(a[s][j]);
+      float y = k3_bf_hi(pv[s][j]) + k3_bf_hi(a[s][j]);
+      if (two) {
+        x += k3_bf_lo(e[s][j]);
+        y += k3_bf_hi(e[s][j]);
+      }
+      o[j] = k3_pack_bf2(x, y);
+    }
+    pv[s] = o;
+  }
+#pragma unroll
+  for (int s = 0; s < K3S_SLOTS; ++s)
+    if (L.valid(s)) k3_st16(hidden + row + L.off(s), pv[s]);
+#endif
+  if (snapshot && NB < K3_NB_MAX) {
+#pragma unroll
+    for (int s = 0; s < K3S_SLOTS; ++s)
+      if (L.valid(s)) k3_st16_nt(blocks + ((size_t)b * K3_NB_MAX + NB) * K3_H + L.off(s), pv[s]);
+  }
+  const K3NormedDst dst = {normed_all + dst_off, dst_peer, dst_off, rank, nr};
+#if K3_PUSH >= 2
+  k3s_attnres_rms_row<NB, K3_MIX_STATS_OUT>(xc, pv, sw, gamma, dst, K3_PUSH_EPS, L, nullptr, 0,
+                                             sw_mlp, stats + (size_t)b * K3_NB_MAX * 2);
+#else
+  k3s_attnres_rms_row<NB, 0>(xc, pv, sw, gamma, dst, K3_PUSH_EPS, L, nullptr, 0);
+#endif
+}
+
+#if K3_PUSH == 3
+#define K3P_PARAMS                                                                          \
+  uint16_t *__restrict__ blocks, const float *__restrict__ sw,                              \
+      const uint16_t *__restrict__ gamma, uint16_t *__restrict__ normed_all,                \
+      const unsigned long long *__restrict__ dst_peer, int nb, int snapshot, int B, int rank, \
+      int nranks, const float *__restrict__ sw_mlp, float *__restrict__ stats,              \
+      const uint16_t *__restrict__ p1, const uint16_t *__restrict__ p2,                     \
+      const uint16_t *__restrict__ prefix2, uint16_t *__restrict__ hidden, int two
+#define K3P_ARGS blocks, sw, gamma, normed_all, dst_peer, snapshot, B, rank, nranks, sw_mlp, \
+                 stats, p1, p2, prefix2, hidden, two
+#elif K3_PUSH == 2
+#define K3P_PARAMS                                                                          \
+  const uint16_t *__restrict__ prefix, uint16_t *__restrict__ blocks,                       \
+      const float *__restrict__ sw, const uint16_t *__restrict__ gamma,                     \
+      uint16_t *__restrict__ normed_all, const unsigned long long *__restrict__ dst_peer,    \
+      int nb, int snapshot, int B, int rank, int nranks, const float *__restrict__ sw_mlp,  \
+      float *__restrict__ stats
+#define K3P_ARGS prefix, blocks, sw, gamma, normed_all, dst_peer, snapshot, B, rank, nranks, \
+                 sw_mlp, stats
+#else
+#define K3P_PARAMS                                                                          \
+  const uint16_t *__restrict__ prefix, uint16_t *__restrict__ blocks,                       \
+      const float *__restrict__ sw, const uint16_t *__restrict__ gamma,                     \
+      uint16_t *__restrict__ normed_all, const unsigned long long *__restrict__ dst_peer,    \
+      int nb, int snapshot, int B, int rank, int nranks
+#define K3P_ARGS prefix, blocks, sw, gamma, normed_all, dst_peer, snapshot, B, rank, nranks
+#endif
+
+// nb is the entry's K (the typed call checks it); the parameter keeps the
+// module entry's list.
+#define K3P_SPLIT_ENTRY(K)                                                                    \
+  extern "C" __global__ void __launch_bounds__(K3S_THREADS)                                   \
+      k3h_attnres_rms_push_nb##K##s(K3P_PARAMS) {                                             \
+    (void)nb;                                                                                 \
+    k3s_push_body<K>(K3P_ARGS);                                                               \
+  }
+K3P_SPLIT_ENTRY(1)
+K3P_SPLIT_ENTRY(2)
+K3P_SPLIT_ENTRY(3)
+K3P_SPLIT_ENTRY(4)
+K3P_SPLIT_ENTRY(5)

@@ -85,8 +85,8 @@ K3_DEV float k3s_row_sumsq_total(const k3_u4* x, float* red, const K3sLane& L) {
 
 // The mix + RMS of one row: pv holds the prefix candidate (the landed prefix2)
 // for the lane's slots; candidates c < NB are read from blk_row.  MODE:
-// 0, or K3_MIX_STATS_IN (the first ns = min(nb_stats, NB) candidates take
-// (sum x^2, sum x * sw) from stats_in, [K3_NB_MAX][2]).
+// 0, K3_MIX_STATS_IN (the first ns = min(nb_stats, NB) candidates take
+// (sum x^2, sum x * sw) from stats_in, [K3_NB_MAX][2]) or K3_MIX_STATS_OUT (below).
 // The candidate rows' loads of the lane's slots (each row is read once:
 // non-temporal), issued by the caller before anything it stores.
 template <int NB>
@@ -98,35 +98,56 @@ K3_DEV void k3s_load_candidates(k3_u4 (&xc)[NB][K3S_SLOTS], const uint16_t* __re
     for (int s = 0; s < K3S_SLOTS; ++s) xc[c][s] = k3_ld16_nt(blk_row + (size_t)c * K3_H + L.off(s));
 }
 
+// MODE also takes K3_MIX_STATS_OUT: every candidate c < NB also accumulates
+// dm_c = sum x * sw_mlp (the same chain and butterfly as dp_c) and
+// stats_out[c] = (sq_c, dm_c) is written (the 128-thread body's half-wave-0 totals:
+// the four per-wave partials summed in wave order).  The normed row goes to every
+// destination of `dst` (the local row and, for the push entries, each peer's).
 template <int NB, int MODE>
 K3_DEV void k3s_attnres_rms_row(const k3_u4 (&xc)[NB][K3S_SLOTS], k3_u4* pv,
                                 const float* __restrict__ sw, const uint16_t* __restrict__ gamma,
-                                uint16_t* __restrict__ normed_row, float eps, const K3sLane& L,
-                                const float* __restrict__ stats_in, int nb_stats) {
+                                const K3NormedDst& dst, float eps, const K3sLane& L,
+                                const float* __restrict__ stats_in, int nb_stats,
+                                const float* __restrict__ sw_mlp = nullptr,
+                                float* __restrict__ stats_out = nullptr) {
   static_assert(NB >= 1 && NB <= K3_NB_MAX, "NB in 1..8");
   constexpr bool SIN = (MODE & K3_MIX_STATS_IN) != 0;
+  constexpr bool SOUT = (MODE & K3_MIX_STATS_OUT) != 0;
   const int ns = SIN ? (nb_stats < 0 ? 0 : nb_stats < NB ? nb_stats : NB) : 0;
   __shared__ float s_red[(NB + 1) * 2 * 4];
+  __shared__ float s_redm[SOUT ? NB * 4 : 1];
   __shared__ float s_red2[4];
-  // sw is shared by every row (cacheable)
-  float4 swv[K3S_SLOTS][2];
+  // sw (and sw_mlp) are shared by every row (cacheable)
+  float4 swv[K3S_SLOTS][2], swm[SOUT ? K3S_SLOTS : 1][2];
 #pragma unroll
   for (int s = 0; s < K3S_SLOTS; ++s) {
     swv[s][0] = *(const float4*)(sw + L.off(s));
     swv[s][1] = *(const float4*)(sw + L.off(s) + 4);
+    if constexpr (SOUT) {
+      swm[s][0] = *(const float4*)(sw_mlp + L.off(s));
+      swm[s][1] = *(const float4*)(sw_mlp + L.off(s) + 4);
+    }
   }
 
   // pass 1: sum x^2 and sum x * sw per candidate (prefix at index NB), chained
   // over the reference thread's steps by the hand-over
-  float sq[NB + 1], dp[NB + 1];
+  float sq[NB + 1], dp[NB + 1], dm[SOUT ? NB : 1];
 #pragma unroll
   for (int c = 0; c <= NB; ++c) { sq[c] = 0.0f; dp[c] = 0.0f; }
+#pragma unroll
+  for (int c = 0; c < (SOUT ? NB : 1); ++c) dm[c] = 0.0f;
   auto run = [&](int n) {
 #pragma unroll
     for (int s = 0; s < K3S_SLOTS; ++s) {
       if (s >= n) break;
       const float wv[8] = {swv[s][0].x, swv[s][0].y, swv[s][0].z, swv[s][0].w,
                            swv[s][1].x, swv[s][1].y, swv[s][1].z, swv[s][1].w};
+      float mv[8];
+      if constexpr (SOUT) {
+        const float4 ma = swm[SOUT ? s : 0][0], mb = swm[SOUT ? s : 0][1];
+        mv[0] = ma.x; mv[1] = ma.y; mv[2] = ma.z; mv[3] = ma.w;
+        mv[4] = mb.x; mv[5] = mb.y; mv[6] = mb.z; mv[7] = mb.w;
+      }
 #pragma unroll
       for (int c = 0; c <= NB; ++c) {
         if (SIN && c < ns) continue;
@@ -138,6 +159,12 @@ K3_DEV void k3s_attnres_rms_row(const k3_u4 (&xc)[NB][K3S_SLOTS], k3_u4* pv,
           sq[c] = __builtin_fmaf(hi, hi, sq[c]);
           dp[c] = __builtin_fmaf(lo, wv[2 * j], dp[c]);
           dp[c] = __builtin_fmaf(hi, wv[2 * j + 1], dp[c]);
+          if constexpr (SOUT) {
+            if (c < NB) {
+              dm[c < NB ? c : 0] = __builtin_fmaf(lo, mv[2 * j], dm[c < NB ? c : 0]);
+              dm[c < NB ? c : 0] = __builtin_fmaf(hi, mv[2 * j + 1], dm[c < NB ? c : 0]);
+            }
+          }
         }
       }
     }
@@ -145,6 +172,8 @@ K3_DEV void k3s_attnres_rms_row(const k3_u4 (&xc)[NB][K3S_SLOTS], k3_u4* pv,
   run(K3S_SLOTS);
 #pragma unroll
   for (int c = 0; c <= NB; ++c) { sq[c] = k3s_handover(sq[c]); dp[c] = k3s_handover(dp[c]); }
+#pragma unroll
+  for (int c = 0; c < (SOUT ? NB : 0); ++c) dm[c] = k3s_handover(dm[c]);
   run(K3_KVPT - K3S_SLOTS);
 #pragma unroll
   for (int c = 0; c <= NB; ++c) {
@@ -152,6 +181,12 @@ K3_DEV void k3s_attnres_rms_row(const k3_u4 (&xc)[NB][K3S_SLOTS], k3_u4* pv,
     const float s = k3_sum32(sq[c]);
     const float d = k3_sum32(dp[c]);
     if (L.lane == 32) { s_red[(2 * c) * 4 + L.w] = s; s_red[(2 * c + 1) * 4 + L.w] = d; }
+    if constexpr (SOUT) {
+      if (c < NB) {
+        const float mm = k3_sum32(dm[c < NB ? c : 0]);
+        if (L.lane == 32) s_redm[c * 4 + L.w] = mm;
+      }
+    }
   }
   __syncthreads();
 
@@ -169,6 +204,15 @@ K3_DEV void k3s_attnres_rms_row(const k3_u4 (&xc)[NB][K3S_SLOTS], k3_u4* pv,
       for (int w = 0; w < 4; ++w) {
         sqv += s_red[(2 * lane32) * 4 + w];
         dpv += s_red[(2 * lane32 + 1) * 4 + w];
+      }
+    }
+    if constexpr (SOUT) {
+      if (L.w == 0 && L.h == 0 && lane32 < NB) {
+        float dmv = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) dmv += s_redm[lane32 * 4 + w];
+        stats_out[2 * lane32] = sqv;
+        stats_out[2 * lane32 + 1] = dmv;
       }
     }
     sc = dpv * k3_row_rscale(sqv, eps);
@@ -209,14 +253,25 @@ K3_DEV void k3s_attnres_rms_row(const k3_u4 (&xc)[NB][K3S_SLOTS], k3_u4* pv,
 
   // RMS of the mixed row, normed = bf16(bf16(mixed * r) (x) gamma)
   const float r = k3_row_rscale(k3s_row_sumsq_total(pv, s_red2, L), eps);
+  k3_u4 nv[K3S_SLOTS];
 #pragma unroll
   for (int s = 0; s < K3S_SLOTS; ++s) {
     const k3_u4 g = k3_ld16(gamma + L.off(s));
-    k3_u4 nv;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      nv[j] = k3_mul_bf2(k3_pack_bf2(k3_bf_lo(pv[s][j]) * r, k3_bf_hi(pv[s][j]) * r), g[j]);
-    if (L.valid(s)) k3_st16_nt(normed_row + L.off(s), nv);
+      nv[s][j] = k3_mul_bf2(k3_pack_bf2(k3_bf_lo(pv[s][j]) * r, k3_bf_hi(pv[s][j]) * r), g[j]);
+    if (L.valid(s)) k3_st16_nt(dst.row + L.off(s), nv[s]);
+  }
+  if (dst.peer) {
+#pragma unroll
+    for (int q = 0; q < K3_MAX_RANKS; ++q) {
+      if (q >= dst.nr) break;
+      if (q == dst.rank) continue;
+      uint16_t* prow = (uint16_t*)(uintptr_t)dst.peer[q] + dst.off;
+#pragma unroll
+      for (int s = 0; s < K3S_SLOTS; ++s)
+        if (L.valid(s)) k3_st16_nt(prow + L.off(s), nv[s]);
+    }
   }
 }
 
@@ -254,7 +309,8 @@ K3_DEV void k3s_land_add_attnres_rms_body(const k3_land_t* __restrict__ partial,
   for (int s = 0; s < K3S_SLOTS; ++s)
     if (L.valid(s)) k3_st16_nt(prefix2 + row + L.off(s), pv[s]);
   const bool have_stats = MODE != 0 && stats != nullptr;
-  k3s_attnres_rms_row<NB, MODE>(xc, pv, sw, gamma, normed + row, K3_EPS, L,
+  const K3NormedDst dst = {normed + row, nullptr, 0, 0, 1};
+  k3s_attnres_rms_row<NB, MODE>(xc, pv, sw, gamma, dst, K3_EPS, L,
                                 have_stats ? stats + (size_t)b * K3_NB_MAX * 2 : nullptr,
                                 have_stats ? nb_stats : 0);
 }

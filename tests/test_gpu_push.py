@@ -66,6 +66,9 @@ class Ranks:
     (3, 0, 16, 0, 4),
     (8, 1, 9, 3, 4),      # nb = 8: no snapshot slot left
     (2, 1, 5, 0, 1),      # one rank: no peers read
+    (1, 1, 11, 2, 4),     # nb 1..5 run the 256-thread split entries
+    (4, 0, 6, 5, 8),
+    (5, 1, 13, 1, 4),
 ])
 def test_attnres_rms_push(ctx, version, nb, snapshot, B, rank, nranks):
     _case(f"push v{version} nb={nb} snapshot={snapshot} B={B} rank={rank}/{nranks}")
@@ -80,7 +83,7 @@ def test_attnres_rms_push(ctx, version, nb, snapshot, B, rank, nranks):
     _eq("blocks", from_dev(blk), wblk)
 
 
-@pytest.mark.parametrize("nb,B", [(0, 8), (1, 33), (5, 16), (8, 7)])
+@pytest.mark.parametrize("nb,B", [(0, 8), (1, 33), (2, 12), (3, 10), (4, 9), (5, 16), (8, 7)])
 def test_attnres_rms_push_stats(ctx, nb, B):
     _case(f"push_stats nb={nb} B={B}")
     _, prefix, _, blocks, sw, sw_mlp, gamma = _inputs(420 + nb, B)
@@ -98,7 +101,8 @@ def test_attnres_rms_push_stats(ctx, nb, B):
     assert (got[:, nb:] == -1.0).all(), "stats past nb written"
 
 
-@pytest.mark.parametrize("nb,two,B", [(0, 1, 12), (4, 0, 21), (7, 1, 8)])
+@pytest.mark.parametrize("nb,two,B", [(0, 1, 12), (1, 1, 9), (2, 0, 10), (3, 1, 6), (4, 0, 21),
+                                      (4, 1, 7), (5, 1, 5), (7, 1, 8)])
 def test_attnres_rms_push_add2(ctx, nb, two, B):
     _case(f"push_add2 nb={nb} two={two} B={B}")
     g, _, _, blocks, sw, sw_mlp, gamma = _inputs(440 + nb, B)
