@@ -553,12 +553,12 @@ def bench_push_land(ctx, add, timed, bf, g, s, O=None, h=None) -> None:
     part = bf(B, HH)
     pre2, nrm = torch.empty_like(part), torch.empty_like(part)
     for k, kern in ((1, "k3h_land_add_attnres_rms_nb1s"), (4, "k3h_land_add_attnres_rms_nb4s"),
-                    (8, "kern_k3_land_add_attnres_rms_nb8")):
+                    (8, "k3h_land_add_attnres_rms_nb8s")):
         add(f"K1b nb {k} (res_mlp, typed call)", kern, f"B={B} nb={k}",
             2 * row + k * row + HH * 4 + HH * 2 + 2 * row,
             timed(lambda k=k: ctx.land_add_attnres_rms_nb(part, prefix, blocks, sw, gm, pre2, nrm, k,
                                                           0, B, stream=s)),
-            "vector-split row body" if k <= 5 else "128-thread row body (reference on GB300: 155 us)",
+            "vector-split row body" + (" (reference on GB300: 155 us)" if k == 8 else ""),
             cpu=O and (lambda a=(h(part), h(prefix), h(blocks), h(sw), h(gm)), k=k:
                        O.land_add_attnres_rms(a[0], a[1], a[2], a[3], a[4], k, 0, B)))
     add("res_mlp nb 5 with res_in statistics (nb_stats 4)", "k3h_land_add_attnres_rms_nb5s",
@@ -672,7 +672,7 @@ OP_KERNELS = {
     "residual push_add2 (res_in, nb 4, 4 ranks)": ["k3h_attnres_rms_push_nb4s"],
     "K1b nb 1 (res_mlp, typed call)": ["k3h_land_add_attnres_rms_nb1s"],
     "K1b nb 4 (res_mlp, typed call)": ["k3h_land_add_attnres_rms_nb4s"],
-    "K1b nb 8 (res_mlp, typed call)": ["kern_k3_land_add_attnres_rms_nb8"],
+    "K1b nb 8 (res_mlp, typed call)": ["k3h_land_add_attnres_rms_nb8s"],
     "res_mlp nb 5 with res_in statistics (nb_stats 4)": ["k3h_land_add_attnres_rms_nb5s"],
     "rms (l0, h 3584)": ["kern_k3_rms"],
     "land (l0, n 3584)": ["kern_k3_land"],

@@ -41,9 +41,10 @@ class K3hArgs {
 int k3h_run(k3h_ctx_t ctx, const char* module_key, const char* entry, uint32_t gx, uint32_t gy,
             uint32_t gz, uint32_t block, void* stream, const K3hArgs& a, uint32_t shmem = 0);
 
-// K1 row bodies: the typed nb entries run the 256-thread vector-split form
-// (k3h_land_add_attnres_rms_nb{K}s) for nb <= kSplitNbMax.
-constexpr int kSplitNbMax = 5;
+// K1 row bodies: the typed nb and push entries run the 256-thread vector-split
+// form (k3h_land_add_attnres_rms_nb{K}s, k3h_attnres_rms_push_nb{K}s) for
+// 1 <= nb <= kSplitNbMax, which covers every nb the row body takes.
+constexpr int kSplitNbMax = 8;
 constexpr uint32_t kSplitThreads = 256;
 
 inline bool k3h_aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }

@@ -49,11 +49,12 @@
 
 // Typed-call entries with no reference counterpart: the same contract on the
 // vector-split row body (k3_residual_split.h), grid (B, 1, 1), block 256:
-//   k3h_land_add_attnres_rms_nb{1..5}s(..., nb_in, snapshot, B[, stats, nb_stats])
-// Measured at B = 4096, cold caches, against the 128-thread entries: nb 1-5
-// 58.3 / 69.0 / 82.8 / 97.2 / 107.7 -> 56.8 / 65.1 / 76.1 / 85.7 / 95.8 us; from
-// nb 6 on the candidates need more than half a SIMD's registers per wave and
-// the split form runs slower (nb 8: 151 -> 220 us), so it is not built there.
+//   k3h_land_add_attnres_rms_nb{1..8}s(..., nb_in, snapshot, B[, stats, nb_stats])
+// Measured at B = 4096 with cold caches, against the 128-thread entries (HIP
+// events, median): nb 1 / 4 / 6 / 8 59.1 / 98.1 / 120.3 / 151.8 -> 58.4 / 85.1 /
+// 109.0 / 131.0 us; after a dirty-cache flush the 128-thread entries, whose
+// pass 2 re-reads candidates through the caches, take 131.9 / 160.4 / 186.6 us
+// at nb 4 / 6 / 8 and the split ones 85.1 / 106.2 / 127.6.
 #ifndef K3_NB_STATS
 #define K3_NBS_ENTRY(K)                                                                     \
   extern "C" __global__ void __launch_bounds__(K3S_THREADS)                              \
@@ -87,6 +88,9 @@ K3_NBS_ENTRY(2)
 K3_NBS_ENTRY(3)
 K3_NBS_ENTRY(4)
 K3_NBS_ENTRY(5)
+K3_NBS_ENTRY(6)
+K3_NBS_ENTRY(7)
+K3_NBS_ENTRY(8)
 
 K3_NB_ENTRY(1)
 K3_NB_ENTRY(2)

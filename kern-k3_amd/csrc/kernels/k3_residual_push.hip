@@ -15,7 +15,7 @@
 //
 // grid (B, 1, 1), block (128, 1, 1) (manifest ceil_div(tokens, 4) rows per rank).
 //
-// Typed-call entries k3h_attnres_rms_push_nb{K}s (K = 1..5, nb == K; same
+// Typed-call entries k3h_attnres_rms_push_nb{K}s (K = 1..8, nb == K; same
 // parameter list as the module's entry, block 256): the vector-split row body
 // (k3_residual_split.h), every candidate held on chip from pass 1 to pass 2,
 // the same bits.
@@ -183,21 +183,23 @@ K3_DEV void k3s_push_body(
     }
     pv[s] = o;
   }
-#pragma unroll
-  for (int s = 0; s < K3S_SLOTS; ++s)
-    if (L.valid(s)) k3_st16(hidden + row + L.off(s), pv[s]);
 #endif
-  if (snapshot && NB < K3_NB_MAX) {
-#pragma unroll
-    for (int s = 0; s < K3S_SLOTS; ++s)
-      if (L.valid(s)) k3_st16_nt(blocks + ((size_t)b * K3_NB_MAX + NB) * K3_H + L.off(s), pv[s]);
-  }
+  // hidden (K3_PUSH 3) and the snapshot slot are stored by the row body once
+  // its own loads are out
   const K3NormedDst dst = {normed_all + dst_off, dst_peer, dst_off, rank, nr};
-#if K3_PUSH >= 2
-  k3s_attnres_rms_row<NB, K3_MIX_STATS_OUT>(xc, pv, sw, gamma, dst, K3_PUSH_EPS, L, nullptr, 0,
-                                             sw_mlp, stats + (size_t)b * K3_NB_MAX * 2);
+  const K3sPvStores pvst = {
+#if K3_PUSH == 3
+      hidden + row,
 #else
-  k3s_attnres_rms_row<NB, 0>(xc, pv, sw, gamma, dst, K3_PUSH_EPS, L, nullptr, 0);
+      nullptr,
+#endif
+      snapshot && NB < K3_NB_MAX ? blocks + ((size_t)b * K3_NB_MAX + NB) * K3_H : nullptr,
+      nullptr};
+#if K3_PUSH >= 2
+  k3s_attnres_rms_row<NB, K3_MIX_STATS_OUT>(xc, pv, sw, gamma, dst, pvst, K3_PUSH_EPS, L, nullptr,
+                                             0, sw_mlp, stats + (size_t)b * K3_NB_MAX * 2);
+#else
+  k3s_attnres_rms_row<NB, 0>(xc, pv, sw, gamma, dst, pvst, K3_PUSH_EPS, L, nullptr, 0);
 #endif
 }
 
@@ -242,3 +244,6 @@ K3P_SPLIT_ENTRY(2)
 K3P_SPLIT_ENTRY(3)
 K3P_SPLIT_ENTRY(4)
 K3P_SPLIT_ENTRY(5)
+K3P_SPLIT_ENTRY(6)
+K3P_SPLIT_ENTRY(7)
+K3P_SPLIT_ENTRY(8)

@@ -20,6 +20,15 @@
 // element-wise (its chain runs over candidates), so each lane mixes its own
 // slots.  The RMS of the mixed row uses the same chain hand-over.
 //
+// Registers decide the speed: at nb 8 the held rows take 128 of a lane's
+// registers, and two waves per SIMD (at most 256 registers) must fit.  Each run
+// over the slots therefore unpacks the held bf16 rows afresh, slot by slot
+// (empty asm statements make the packed rows the only live copy), instead of
+// keeping the unpacked floats of one run alive into the next: 408 -> 208
+// registers at nb 8 (1 -> 2 waves per SIMD), 209 -> 147 at nb 4 (2 -> 3).
+// The prefix-row stores (prefix2, hidden, the snapshot slot) follow the row
+// body's own loads (sw, sw_mlp, gamma): no load waits behind a store.
+//
 // Launch: block 256, one row per workgroup (grid B).  No reference entry uses
 // this geometry; the manifest entries keep the 128-thread body.
 #pragma once
@@ -83,6 +92,16 @@ K3_DEV float k3s_row_sumsq_total(const k3_u4* x, float* red, const K3sLane& L) {
   return tot;
 }
 
+// Stores of the prefix candidate (prefix2, hidden, the snapshot slot) that the
+// row body issues once its own loads (sw, sw_mlp) are out, so that no load
+// waits behind them (the vector memory counter retires in order and counts
+// stores): `cached` goes through the caches, `nt0` and `nt1` are non-temporal.
+struct K3sPvStores {
+  uint16_t* cached;
+  uint16_t* nt0;
+  uint16_t* nt1;
+};
+
 // The mix + RMS of one row: pv holds the prefix candidate (the landed prefix2)
 // for the lane's slots; candidates c < NB are read from blk_row.  MODE:
 // 0, K3_MIX_STATS_IN (the first ns = min(nb_stats, NB) candidates take
@@ -104,11 +123,11 @@ K3_DEV void k3s_load_candidates(k3_u4 (&xc)[NB][K3S_SLOTS], const uint16_t* __re
 // the four per-wave partials summed in wave order).  The normed row goes to every
 // destination of `dst` (the local row and, for the push entries, each peer's).
 template <int NB, int MODE>
-K3_DEV void k3s_attnres_rms_row(const k3_u4 (&xc)[NB][K3S_SLOTS], k3_u4* pv,
+K3_DEV void k3s_attnres_rms_row(k3_u4 (&xc)[NB][K3S_SLOTS], k3_u4* pv,
                                 const float* __restrict__ sw, const uint16_t* __restrict__ gamma,
-                                const K3NormedDst& dst, float eps, const K3sLane& L,
-                                const float* __restrict__ stats_in, int nb_stats,
-                                const float* __restrict__ sw_mlp = nullptr,
+                                const K3NormedDst& dst, const K3sPvStores& pvst, float eps,
+                                const K3sLane& L, const float* __restrict__ stats_in,
+                                int nb_stats, const float* __restrict__ sw_mlp = nullptr,
                                 float* __restrict__ stats_out = nullptr) {
   static_assert(NB >= 1 && NB <= K3_NB_MAX, "NB in 1..8");
   constexpr bool SIN = (MODE & K3_MIX_STATS_IN) != 0;
@@ -129,6 +148,22 @@ K3_DEV void k3s_attnres_rms_row(const k3_u4 (&xc)[NB][K3S_SLOTS], k3_u4* pv,
     }
   }
 
+  // gamma is loaded with sw where the registers allow it (measured: the
+  // statistics-writing push entries and nb above 6 lose occupancy), otherwise
+  // at the normed stores
+  constexpr bool GEARLY = !SOUT && NB <= 6;
+  k3_u4 gv[K3S_SLOTS];
+  if constexpr (GEARLY) {
+#pragma unroll
+    for (int s = 0; s < K3S_SLOTS; ++s) gv[s] = k3_ld16(gamma + L.off(s));
+  }
+#pragma unroll
+  for (int s = 0; s < K3S_SLOTS; ++s) {
+    if (!L.valid(s)) continue;
+    if (pvst.cached) k3_st16(pvst.cached + L.off(s), pv[s]);
+    if (pvst.nt0) k3_st16_nt(pvst.nt0 + L.off(s), pv[s]);
+    if (pvst.nt1) k3_st16_nt(pvst.nt1 + L.off(s), pv[s]);
+  }
   // pass 1: sum x^2 and sum x * sw per candidate (prefix at index NB), chained
   // over the reference thread's steps by the hand-over
   float sq[NB + 1], dp[NB + 1], dm[SOUT ? NB : 1];
@@ -167,14 +202,37 @@ K3_DEV void k3s_attnres_rms_row(const k3_u4 (&xc)[NB][K3S_SLOTS], k3_u4* pv,
           }
         }
       }
+      // slot by slot: the next slot is unpacked after this slot's chains
+#pragma unroll
+      for (int c = 0; c <= NB; ++c) asm volatile("" : "+v"(sq[c]), "+v"(dp[c]));
+#pragma unroll
+      for (int c = 0; c < (SOUT ? NB : 0); ++c) asm volatile("" : "+v"(dm[c]));
+      if (s + 1 < n) {
+#pragma unroll
+        for (int c = 0; c < NB; ++c) asm volatile("" : "+v"(xc[c][s + 1 < K3S_SLOTS ? s + 1 : 0]));
+        asm volatile("" : "+v"(pv[s + 1 < K3S_SLOTS ? s + 1 : 0]));
+      }
     }
+  };
+  // Each use of a held row unpacks it again: the empty asm makes the packed
+  // form the only live copy, so the unpacked floats of one run (twice the
+  // registers) are not kept alive into the next run or pass 2.
+  auto pin = [&]() {
+#pragma unroll
+    for (int c = 0; c < NB; ++c)
+#pragma unroll
+      for (int s = 0; s < K3S_SLOTS; ++s) asm volatile("" : "+v"(xc[c][s]));
+#pragma unroll
+    for (int s = 0; s < K3S_SLOTS; ++s) asm volatile("" : "+v"(pv[s]));
   };
   run(K3S_SLOTS);
 #pragma unroll
   for (int c = 0; c <= NB; ++c) { sq[c] = k3s_handover(sq[c]); dp[c] = k3s_handover(dp[c]); }
 #pragma unroll
   for (int c = 0; c < (SOUT ? NB : 0); ++c) dm[c] = k3s_handover(dm[c]);
+  pin();
   run(K3_KVPT - K3S_SLOTS);
+  pin();
 #pragma unroll
   for (int c = 0; c <= NB; ++c) {
     if (SIN && c < ns) continue;
@@ -249,6 +307,11 @@ K3_DEV void k3s_attnres_rms_row(const k3_u4 (&xc)[NB][K3S_SLOTS], k3_u4* pv,
       }
 #pragma unroll
     for (int j = 0; j < 4; ++j) pv[s][j] = k3_pack_bf2(acc[2 * j], acc[2 * j + 1]);
+    asm volatile("" : "+v"(pv[s]));
+    if (s + 1 < K3S_SLOTS) {
+#pragma unroll
+      for (int c = 0; c < NB; ++c) asm volatile("" : "+v"(xc[c][s + 1 < K3S_SLOTS ? s + 1 : 0]));
+    }
   }
 
   // RMS of the mixed row, normed = bf16(bf16(mixed * r) (x) gamma)
@@ -256,7 +319,7 @@ K3_DEV void k3s_attnres_rms_row(const k3_u4 (&xc)[NB][K3S_SLOTS], k3_u4* pv,
   k3_u4 nv[K3S_SLOTS];
 #pragma unroll
   for (int s = 0; s < K3S_SLOTS; ++s) {
-    const k3_u4 g = k3_ld16(gamma + L.off(s));
+    const k3_u4 g = GEARLY ? gv[s] : k3_ld16(gamma + L.off(s));
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       nv[s][j] = k3_mul_bf2(k3_pack_bf2(k3_bf_lo(pv[s][j]) * r, k3_bf_hi(pv[s][j]) * r), g[j]);
@@ -305,12 +368,10 @@ K3_DEV void k3s_land_add_attnres_rms_body(const k3_land_t* __restrict__ partial,
 #pragma unroll
     for (int s = 0; s < K3S_SLOTS; ++s) pv[s] = k3_add_land(pr[s], pv[s]);
   }
-#pragma unroll
-  for (int s = 0; s < K3S_SLOTS; ++s)
-    if (L.valid(s)) k3_st16_nt(prefix2 + row + L.off(s), pv[s]);
   const bool have_stats = MODE != 0 && stats != nullptr;
   const K3NormedDst dst = {normed + row, nullptr, 0, 0, 1};
-  k3s_attnres_rms_row<NB, MODE>(xc, pv, sw, gamma, dst, K3_EPS, L,
+  const K3sPvStores pvst = {nullptr, prefix2 + row, nullptr};
+  k3s_attnres_rms_row<NB, MODE>(xc, pv, sw, gamma, dst, pvst, K3_EPS, L,
                                 have_stats ? stats + (size_t)b * K3_NB_MAX * 2 : nullptr,
                                 have_stats ? nb_stats : 0);
 }
