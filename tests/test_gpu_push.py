@@ -66,9 +66,11 @@ class Ranks:
     (3, 0, 16, 0, 4),
     (8, 1, 9, 3, 4),      # nb = 8: no snapshot slot left
     (2, 1, 5, 0, 1),      # one rank: no peers read
-    (1, 1, 11, 2, 4),     # nb 1..5 run the 256-thread split entries
+    (1, 1, 11, 2, 4),     # nb 1..8 run the 256-thread split entries
     (4, 0, 6, 5, 8),
     (5, 1, 13, 1, 4),
+    (6, 1, 7, 2, 4),
+    (7, 0, 10, 0, 8),
 ])
 def test_attnres_rms_push(ctx, version, nb, snapshot, B, rank, nranks):
     _case(f"push v{version} nb={nb} snapshot={snapshot} B={B} rank={rank}/{nranks}")
@@ -83,7 +85,8 @@ def test_attnres_rms_push(ctx, version, nb, snapshot, B, rank, nranks):
     _eq("blocks", from_dev(blk), wblk)
 
 
-@pytest.mark.parametrize("nb,B", [(0, 8), (1, 33), (2, 12), (3, 10), (4, 9), (5, 16), (8, 7)])
+@pytest.mark.parametrize("nb,B", [(0, 8), (1, 33), (2, 12), (3, 10), (4, 9), (5, 16), (6, 5), (7, 11),
+                                  (8, 7)])
 def test_attnres_rms_push_stats(ctx, nb, B):
     _case(f"push_stats nb={nb} B={B}")
     _, prefix, _, blocks, sw, sw_mlp, gamma = _inputs(420 + nb, B)
@@ -102,7 +105,7 @@ def test_attnres_rms_push_stats(ctx, nb, B):
 
 
 @pytest.mark.parametrize("nb,two,B", [(0, 1, 12), (1, 1, 9), (2, 0, 10), (3, 1, 6), (4, 0, 21),
-                                      (4, 1, 7), (5, 1, 5), (7, 1, 8)])
+                                      (4, 1, 7), (5, 1, 5), (6, 0, 9), (7, 1, 8), (8, 1, 6)])
 def test_attnres_rms_push_add2(ctx, nb, two, B):
     _case(f"push_add2 nb={nb} two={two} B={B}")
     g, _, _, blocks, sw, sw_mlp, gamma = _inputs(440 + nb, B)
@@ -123,7 +126,7 @@ def test_attnres_rms_push_add2(ctx, nb, two, B):
     _eq("stats", from_dev(stats)[:, :nb].view(np.uint32), wst[:, :nb].view(np.uint32))
 
 
-@pytest.mark.parametrize("nb", [1, 2, 4, 5, 8])
+@pytest.mark.parametrize("nb", range(1, 9))
 def test_nb_stats_consumer(ctx, nb):
     """res_mlp's nb entries with res_in's statistics: bit-exact with the oracle for
     every nb_stats, and -- given statistics computed with sw_mlp = res_mlp's sw --
@@ -183,6 +186,31 @@ def test_push_full_rank_share(ctx):
     _, wn = O.attnres_rms(prefix, None, None, gamma, 0, 0, B)
     R.check(1, wn)
     _eq("blocks[:, 0]", from_dev(blocks)[:, 0], prefix)
+
+
+@pytest.mark.parametrize("nb", [4, 8])
+def test_push_add2_full_rank_share(ctx, nb):
+    """push_add2 at one rank's share of the 16k prefill (B = 4096 rows, the
+    benchmarked shape), every row bit-exact: hidden, every rank's normed copy,
+    the snapshot slot and the statistics."""
+    B = 4096
+    _case(f"push_add2 nb={nb} at B={B}")
+    g, _, _, blocks, sw, sw_mlp, gamma = _inputs(470 + nb, B)
+    p1, p2, prefix2 = (normal_bf16(g, (B, H)) for _ in range(3))
+    R = Ranks(4, B)
+    stats = torch.zeros((B, 8, 2), dtype=torch.float32, device="cuda")
+    hidden = torch.empty((B, H), dtype=torch.bfloat16, device="cuda")
+    blk = to_dev(blocks)
+    ctx.attnres_rms_push_add2(blk, to_dev(sw), to_dev(gamma), R.bufs[3], R.peer, nb, 1, B, 3, 4,
+                              to_dev(sw_mlp), stats, to_dev(p1), to_dev(p2), to_dev(prefix2),
+                              hidden, 1)
+    torch.cuda.synchronize()
+    wh = O.land_add2_bf16(p1, p2, prefix2, 1, B)
+    _eq("hidden", from_dev(hidden), wh)
+    wblk, wn, wst = O.attnres_rms_stats(wh, blocks, sw, gamma, nb, 1, B, sw_mlp=sw_mlp)
+    R.check(3, wn)
+    _eq("blocks", from_dev(blk), wblk)
+    _eq("stats", from_dev(stats)[:, :nb].view(np.uint32), wst[:, :nb].view(np.uint32))
 
 
 def test_manifest_push_ops(ctx):

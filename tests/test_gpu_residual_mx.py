@@ -88,6 +88,23 @@ def test_k1b_per_nb_entries(ctx, nb):
     _eq("normed", from_dev(nrm), want_n)
 
 
+@pytest.mark.parametrize("nb", [4, 8])
+def test_k1b_per_nb_full_rank_share(ctx, nb):
+    """The typed nb entry at the benchmarked shape (B = 4096 rows of one rank's
+    16k-prefill share), every row bit-exact."""
+    B = 4096
+    _case(f"k1b_nb{nb} at B={B}")
+    prefix, partial, blocks, sw, gamma = _k1_inputs(320 + nb, B)
+    want_p2, want_n = O.land_add_attnres_rms(partial, prefix, blocks, sw, gamma, nb, 0, B)
+    p2 = torch.empty((B, H), dtype=torch.bfloat16, device="cuda")
+    nrm = torch.empty_like(p2)
+    ctx.land_add_attnres_rms_nb(to_dev(partial), to_dev(prefix), to_dev(blocks), to_dev(sw),
+                                to_dev(gamma), p2, nrm, nb, 0, B)
+    torch.cuda.synchronize()
+    _eq("prefix2", from_dev(p2), want_p2)
+    _eq("normed", from_dev(nrm), want_n)
+
+
 @pytest.mark.parametrize("nb,snapshot", [(0, 0), (0, 1), (3, 1), (7, 1), (8, 1), (4, 0)])
 def test_k1a_attnres_rms(ctx, nb, snapshot):
     B = 10
