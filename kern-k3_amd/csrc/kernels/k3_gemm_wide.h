@@ -82,15 +82,6 @@ K3_DEV void k3w_wait_vm(int n) {
   else __builtin_amdgcn_s_waitcnt(K3W_VMCNT(0));
 }
 
-// Exchange between the half-waves: x keeps lanes 0-31 and takes y's lanes 0-31
-// into lanes 32-63; y keeps lanes 32-63 and takes x's lanes 32-63 into lanes
-// 0-31 (v_permlane32_swap x, y).
-K3_DEV void k3w_swap(uint32_t& x, uint32_t& y) {
-  const auto r = __builtin_amdgcn_permlane32_swap(x, y, false, false);
-  x = r[0];
-  y = r[1];
-}
-
 // One work item (wave-uniform): its slot in the workgroup's list, route tile,
 // 512-column block and expert.
 struct K3wItem {
@@ -374,10 +365,10 @@ K3_DEV void k3w_gemm_bf16(K3G_PARAMS, uint16_t* __restrict__ out) {
         uint32_t d[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) d[k] = k3_pack_bf2(acc[mt][nt][2 * k], acc[mt][nt][2 * k + 1]);
-        k3w_swap(d[0], d[4]);
-        k3w_swap(d[1], d[5]);
-        k3w_swap(d[2], d[6]);
-        k3w_swap(d[3], d[7]);
+        k3g_swap(d[0], d[4]);
+        k3g_swap(d[1], d[5]);
+        k3g_swap(d[2], d[6]);
+        k3g_swap(d[3], d[7]);
         uint16_t* o = out + K3W_LANE_ROW(mt) * N + K3W_TILE_COL(nt) + 16 * h;
         k3_st16(o, (k3_u4){d[0], d[1], d[4], d[5]});
         k3_st16(o + 8, (k3_u4){d[2], d[3], d[6], d[7]});
