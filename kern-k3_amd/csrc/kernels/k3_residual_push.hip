@@ -42,6 +42,22 @@
 
 #if K3_PUSH == 3
 // hidden = bf16(f32(prefix2) + f32(p1) [+ f32(p2)]) for this thread's vectors.
+// hidden = bf16(f32(prefix2) + f32(p1) [+ f32(p2)]), left to right, one rounding
+K3_DEV k3_u4 k3_add2_vec(k3_u4 pv, k3_u4 a, k3_u4 e, int two) {
+  k3_u4 o;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float x = k3_bf_lo(pv[j]) + k3_bf_lo(a[j]);
+    float y = k3_bf_hi(pv[j]) + k3_bf_hi(a[j]);
+    if (two) {
+      x += k3_bf_lo(e[j]);
+      y += k3_bf_hi(e[j]);
+    }
+    o[j] = k3_pack_bf2(x, y);
+  }
+  return o;
+}
+
 K3_DEV void k3_push_land_add2(const uint16_t* __restrict__ p1, const uint16_t* __restrict__ p2,
                               const uint16_t* __restrict__ prefix2, uint16_t* __restrict__ hidden,
                               int two, size_t row, int t, k3_u4* pv) {
@@ -57,20 +73,7 @@ K3_DEV void k3_push_land_add2(const uint16_t* __restrict__ p1, const uint16_t* _
     for (int v = 0; v < K3_KVPT; ++v) e[v] = k3_ld16_nt(p2 + row + k3_vec_off(t, v));
   }
 #pragma unroll
-  for (int v = 0; v < K3_KVPT; ++v) {
-    k3_u4 o;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float x = k3_bf_lo(pv[v][j]) + k3_bf_lo(a[v][j]);
-      float y = k3_bf_hi(pv[v][j]) + k3_bf_hi(a[v][j]);
-      if (two) {
-        x += k3_bf_lo(e[v][j]);
-        y += k3_bf_hi(e[v][j]);
-      }
-      o[j] = k3_pack_bf2(x, y);
-    }
-    pv[v] = o;
-  }
+  for (int v = 0; v < K3_KVPT; ++v) pv[v] = k3_add2_vec(pv[v], a[v], e[v], two);
 #pragma unroll
   for (int v = 0; v < K3_KVPT; ++v) k3_st16(hidden + row + k3_vec_off(t, v), pv[v]);
 }
@@ -99,6 +102,66 @@ extern "C" __global__ void __launch_bounds__(K3_RES_THREADS) kern_k3_attnres_rms
   const int nr = nranks < K3_MAX_RANKS ? nranks : K3_MAX_RANKS;
   const long long dst_off = ((long long)rank * B + b) * K3_H;
   const size_t row = (size_t)b * K3_H;
+
+  if (nb == 0) {
+    // the first layer's res_in (the mix is the identity): every load of the row
+    // first (the prefix or its land_add2 operands, gamma), the reduction, then
+    // the stores (hidden, the snapshot slot, the normed copies), so that no load
+    // waits behind a store; the arithmetic of the general body at nb == 0
+    __shared__ float s_red0[K3_NHW];
+    k3_u4 pv[K3_KVPT], g[K3_KVPT];
+#if K3_PUSH == 3
+    k3_u4 a[K3_KVPT], e[K3_KVPT];
+#pragma unroll
+    for (int v = 0; v < K3_KVPT; ++v) {
+      a[v] = k3_ld16_nt(p1 + row + k3_vec_off(t, v));
+      pv[v] = k3_ld16_nt(prefix2 + row + k3_vec_off(t, v));
+    }
+    if (two) {
+#pragma unroll
+      for (int v = 0; v < K3_KVPT; ++v) e[v] = k3_ld16_nt(p2 + row + k3_vec_off(t, v));
+    }
+#else
+#pragma unroll
+    for (int v = 0; v < K3_KVPT; ++v) pv[v] = k3_ld16_nt(prefix + row + k3_vec_off(t, v));
+#endif
+#pragma unroll
+    for (int v = 0; v < K3_KVPT; ++v) g[v] = k3_ld16(gamma + k3_vec_off(t, v));
+#if K3_PUSH == 3
+#pragma unroll
+    for (int v = 0; v < K3_KVPT; ++v) pv[v] = k3_add2_vec(pv[v], a[v], e[v], two);
+#endif
+    const float r = k3_row_rscale(k3_block_sum128(k3_row_sumsq(pv), s_red0, t), K3_PUSH_EPS);
+#if K3_PUSH == 3
+#pragma unroll
+    for (int v = 0; v < K3_KVPT; ++v) k3_st16(hidden + row + k3_vec_off(t, v), pv[v]);
+#endif
+    if (snapshot) {
+#pragma unroll
+      for (int v = 0; v < K3_KVPT; ++v)
+        k3_st16_nt(blocks + (size_t)b * K3_NB_MAX * K3_H + k3_vec_off(t, v), pv[v]);
+    }
+    k3_u4 nv[K3_KVPT];
+#pragma unroll
+    for (int v = 0; v < K3_KVPT; ++v)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        nv[v][j] = k3_mul_bf2(k3_pack_bf2(k3_bf_lo(pv[v][j]) * r, k3_bf_hi(pv[v][j]) * r), g[v][j]);
+    uint16_t* lrow = normed_all + dst_off;
+#pragma unroll
+    for (int v = 0; v < K3_KVPT; ++v) k3_st16_nt(lrow + k3_vec_off(t, v), nv[v]);
+    if (dst_peer) {
+#pragma unroll
+      for (int q = 0; q < K3_MAX_RANKS; ++q) {
+        if (q >= nr) break;
+        if (q == rank) continue;
+        uint16_t* prow = (uint16_t*)(uintptr_t)dst_peer[q] + dst_off;
+#pragma unroll
+        for (int v = 0; v < K3_KVPT; ++v) k3_st16_nt(prow + k3_vec_off(t, v), nv[v]);
+      }
+    }
+    return;
+  }
 
   k3_u4 pv[K3_KVPT];
 #if K3_PUSH == 3
@@ -167,22 +230,8 @@ K3_DEV void k3s_push_body(
   k3_u4 xc[NB][K3S_SLOTS];
   k3s_load_candidates<NB>(xc, blocks + (size_t)b * K3_NB_MAX * K3_H, L);
 #if K3_PUSH == 3
-  // hidden = bf16(f32(prefix2) + f32(p1) [+ f32(p2)]), left to right, one rounding
 #pragma unroll
-  for (int s = 0; s < K3S_SLOTS; ++s) {
-    k3_u4 o;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float x = k3_bf_lo(pv[s][j]) + k3_bf_lo(a[s][j]);
-      float y = k3_bf_hi(pv[s][j]) + k3_bf_hi(a[s][j]);
-      if (two) {
-        x += k3_bf_lo(e[s][j]);
-        y += k3_bf_hi(e[s][j]);
-      }
-      o[j] = k3_pack_bf2(x, y);
-    }
-    pv[s] = o;
-  }
+  for (int s = 0; s < K3S_SLOTS; ++s) pv[s] = k3_add2_vec(pv[s], a[s], e[s], two);
 #endif
   // hidden (K3_PUSH 3) and the snapshot slot are stored by the row body once
   // its own loads are out
