@@ -158,3 +158,23 @@ def test_permute_and_shuffles():
     s2 = g.integers(0, 256, (2 * n * kg,), dtype=np.uint8)
     d2 = O.moe_sf_shuffle(s2, 2, n, kg, 0)
     assert sorted(d2.tolist()) == sorted(s2.tolist())
+
+
+@pytest.mark.parametrize("gated", [0, 1])
+def test_sf_shuffle_byte_placement(gated):
+    """kern_k3_moe_sf_shuffle's destination layout (k3_moe_prefill_v4.cu:320-327),
+    restated by reshapes instead of the oracle's index formula: the scale rows
+    first take the weight shuffle's row order (read off the separately pinned
+    moe_w_shuffle), then every 128-row block x 4-column group forms one 512-byte
+    unit ordered [row % 32][(row % 128) / 32][column % 4]."""
+    E, n, kg = 2, 256, 12
+    g = rng(77 + gated)
+    src = g.integers(0, 256, (E, n, kg), dtype=np.uint8)
+    # the row each destination row reads, from moe_w_shuffle over tagged rows
+    tags = np.repeat(np.arange(E * n, dtype=np.uint16), 8).view(np.uint8).reshape(E * n, 16)
+    perm = O.moe_w_shuffle(np.ascontiguousarray(tags), E, n, 16, gated).view(np.uint16)[:, 0]
+    perm = perm.reshape(E, n) - (np.arange(E) * n)[:, None]
+    rows = np.take_along_axis(src, perm[:, :, None].astype(np.int64), axis=1)   # [E, n, kg]
+    want = rows.reshape(E, n // 128, 4, 32, kg // 4, 4).transpose(0, 1, 4, 3, 2, 5).reshape(E, -1)
+    got = O.moe_sf_shuffle(np.ascontiguousarray(src.reshape(-1)), E, n, kg, gated).reshape(E, -1)
+    assert np.array_equal(got, want)

@@ -184,3 +184,38 @@ def test_quant_fp8_pair_against_numpy(v2):
     want = torch.from_numpy(np.clip(bf16_to_f32(x) * inv, -448, 448).astype(np.float32)).to(
         torch.float8_e4m3fn).view(torch.uint8).numpy()
     assert np.array_equal(y, want)
+
+
+@pytest.mark.parametrize("v2,n,nb", [(0, 7168 * 40 + 5, 64), (1, 7168 * 40 + 5, 64), (1, 8 * 256 * 3 + 3, 2),
+                                     (0, 1000, 3)])
+def test_quant_fp8_amax_partials_per_block(v2, n, nb):
+    """Every amax partial, not only their maximum: block b's slice of the grid
+    stride (kern_quant_fp8_amax: elements (i // 256) % nb == b; _v2: 8-element
+    vectors (i // 8 // 256) % nb == b, the n % 8 tail in block 0), restated by
+    reshapes over a zero-padded |x|."""
+    g = rng(90 + v2 + n % 7)
+    x = normal_bf16(g, (n,), outlier_p=0.01)
+    a = np.abs(bf16_to_f32(x))
+    got = O.quant_fp8_amax(x, n, nb, v2=bool(v2))
+    if not v2:
+        stride = nb * 256
+        pad = np.zeros(-(-n // stride) * stride, np.float32)
+        pad[:n] = a
+        want = pad.reshape(-1, nb, 256).max(axis=(0, 2))
+    else:
+        nv = n // 8
+        stride = nb * 256
+        pad = np.zeros(-(-nv // stride) * stride * 8, np.float32)
+        pad[:nv * 8] = a[:nv * 8]
+        want = pad.reshape(-1, nb, 256 * 8).max(axis=(0, 2))
+        if n % 8:
+            want[0] = max(want[0], a[nv * 8:].max())
+    assert np.array_equal(got, want.astype(np.float32))
+    # a planted change of one element moves exactly its own block's partial
+    i = n // 3
+    y = x.copy()
+    y[i] = 0x7f00  # bf16 1.7e38, larger than every other |x|
+    b = (i // 256) % nb if not v2 else ((i // 8) // 256) % nb if i < (n // 8) * 8 else 0
+    got2 = O.quant_fp8_amax(y, n, nb, v2=bool(v2))
+    changed = np.nonzero(got2 != got)[0].tolist()
+    assert changed == [b]
