@@ -27,13 +27,12 @@ K3_DEV uint32_t k3_vec_absmax_bits(k3_u4 v) {
 }
 
 // Scale eight bf16 by 2^-e and convert to e4m3: two words, byte k = value k.
-K3_DEV k3_u2 k3_vec_to_e4m3(k3_u4 v, int e) {
+// e4m3 codes of eight values already in f32 (x * 2^-e for the block exponent e;
+// x bf16-representable), in order.
+K3_DEV k3_u2 k3_f8_to_e4m3(const float (&x)[8], int e) {
   float f[8];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    f[2 * j] = __builtin_ldexpf(k3_bf_lo(v[j]), -e);
-    f[2 * j + 1] = __builtin_ldexpf(k3_bf_hi(v[j]), -e);
-  }
+  for (int k = 0; k < 8; ++k) f[k] = __builtin_ldexpf(x[k], -e);
   k3_u2 o;
   o[0] = k3_pack_e4m3x4(f[0], f[1], f[2], f[3]);
   o[1] = k3_pack_e4m3x4(f[4], f[5], f[6], f[7]);
@@ -50,6 +49,16 @@ K3_DEV k3_u2 k3_vec_to_e4m3(k3_u4 v, int e) {
     }
   }
   return o;
+}
+
+K3_DEV k3_u2 k3_vec_to_e4m3(k3_u4 v, int e) {
+  float x[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    x[2 * j] = k3_bf_lo(v[j]);
+    x[2 * j + 1] = k3_bf_hi(v[j]);
+  }
+  return k3_f8_to_e4m3(x, e);
 }
 
 // Quantise the 16-byte vector this lane holds; the quad's block exponent is

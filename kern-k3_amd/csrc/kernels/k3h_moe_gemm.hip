@@ -532,24 +532,33 @@ K3_DEV void k3g_gemm_situ_mx(K3G_PARAMS, uint8_t* __restrict__ out_q, uint8_t* _
       uint32_t sfp = 0;
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        uint32_t xb[8];  // bf16 activations, q order, two per dword
+        // bf16 activations in q order, as f32; their block amax in f32 (the max of
+        // bf16 values is a bf16 value, NaN ignored as in kern_k3_moe_quant)
+        float xr[16];
+        float am = 0.0f;
 #pragma unroll
         for (int q = 0; q < 16; q += 2) {
+          const uint32_t u2 = k3_pack_bf2(acc[mt][2 * p][q], acc[mt][2 * p][q + 1]);
+          const uint32_t g2 = k3_pack_bf2(acc[mt][2 * p + 1][q], acc[mt][2 * p + 1][q + 1]);
           float x[2];
 #pragma unroll
           for (int d = 0; d < 2; ++d) {
-            const float u = k3_land(acc[mt][2 * p][q + d]);
-            const float g = k3_land(acc[mt][2 * p + 1][q + d]);
+            const float u = d ? k3_bf_hi(u2) : k3_bf_lo(u2);
+            const float g = d ? k3_bf_hi(g2) : k3_bf_lo(g2);
             x[d] = k3c ? k3_situ(g, u) : k3_situ_gate_a(g, al, ial) * k3_situ_up_b(u, be, ibe);
           }
-          xb[q / 2] = k3_pack_bf2(x[0], x[1]);
+          const uint32_t xb = k3_pack_bf2(x[0], x[1]);
+          xr[q] = k3_bf_lo(xb);
+          xr[q + 1] = k3_bf_hi(xb);
+          am = __builtin_fmaxf(am, __builtin_fabsf(xr[q]));
+          am = __builtin_fmaxf(am, __builtin_fabsf(xr[q + 1]));
         }
-        const k3_u4 v0 = {xb[0], xb[1], xb[2], xb[3]}, v1 = {xb[4], xb[5], xb[6], xb[7]};
-        const uint32_t m0 = k3_vec_absmax_bits(v0), m1 = k3_vec_absmax_bits(v1);
-        uint32_t mx = m0 > m1 ? m0 : m1, my = mx;
+        uint32_t mx = __float_as_uint(am) >> 16, my = mx;
         k3g_swap(mx, my);  // mx: lane l % 32's amax, my: lane 32 + l % 32's
         const int ex = k3_e8m0_exp(mx > my ? mx : my);
-        const k3_u2 c0 = k3_vec_to_e4m3(v0, ex), c1 = k3_vec_to_e4m3(v1, ex);
+        const float(&x0)[8] = *reinterpret_cast<const float(*)[8]>(&xr[0]);
+        const float(&x1)[8] = *reinterpret_cast<const float(*)[8]>(&xr[8]);
+        const k3_u2 c0 = k3_f8_to_e4m3(x0, ex), c1 = k3_f8_to_e4m3(x1, ex);
         // code dwords: columns 4 h + 0..3, 8 + 4 h.., 16 + 4 h.., 24 + 4 h..
         uint32_t d0 = c0[0], d1 = c0[1], d2 = c1[0], d3 = c1[1];
         k3g_swap(d0, d2);
