@@ -505,14 +505,51 @@ K3_DEV void k3g_gemm_bf16(K3G_PARAMS, uint16_t* __restrict__ out) {
 }
 
 // fc1 epilogue, on the swapped accumulator layout (no LDS): lane (j, h) holds,
-// for each m tile mt and activation tile p (logical tiles 4 wn + 2 p: up, and
-// 4 wn + 2 p + 1: gate), the 16 activation columns 8 (q / 4) + 4 h + q % 4 of
-// row 32 (2 wm + mt) + j.  The 32-column MX block of (row, p) is the lane pair
-// (l, l ^ 32): the block amax takes one exchange (v_permlane32_swap), the e4m3
-// codes are quantised in registers as kern_k3_moe_quant does (block amax of
-// the bf16 patterns, E8M0 exponent, e4m3 of x * 2^-e), and two exchanges of
-// code dwords leave lane (j, h) with columns 16 h .. + 16 of the block: one
-// 16-byte store per lane and block, one 2-byte scale store per row.
+// for each m tile and activation tile (logical tiles 2 p: up, and 2 p + 1: gate,
+// within the wave's four), the 16 activation columns 8 (q / 4) + 4 h + q % 4 of
+// one row.  The 32-column MX block of (row, p) is the lane pair (l, l ^ 32):
+// the block amax takes one exchange (v_permlane32_swap), the e4m3 codes are
+// quantised in registers as kern_k3_moe_quant does (block amax of the bf16
+// activations, E8M0 exponent, e4m3 of x * 2^-e), and two exchanges of code
+// dwords leave lane (j, h) with columns 16 h .. + 16 of the block: one 16-byte
+// store per lane and block.  Returns the block's E8M0 byte.
+K3_DEV uint32_t k3g_situ_block(const k3_v16f& up, const k3_v16f& gate, bool k3c, float al,
+                               float ial, float be, float ibe, uint8_t* __restrict__ o, int h) {
+  // bf16 activations in q order, as f32; their block amax in f32 (the max of
+  // bf16 values is a bf16 value, NaN ignored as in kern_k3_moe_quant)
+  float xr[16];
+  float am = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 16; q += 2) {
+    const uint32_t u2 = k3_pack_bf2(up[q], up[q + 1]);
+    const uint32_t g2 = k3_pack_bf2(gate[q], gate[q + 1]);
+    float x[2];
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      const float u = d ? k3_bf_hi(u2) : k3_bf_lo(u2);
+      const float g = d ? k3_bf_hi(g2) : k3_bf_lo(g2);
+      x[d] = k3c ? k3_situ(g, u) : k3_situ_gate_a(g, al, ial) * k3_situ_up_b(u, be, ibe);
+    }
+    const uint32_t xb = k3_pack_bf2(x[0], x[1]);
+    xr[q] = k3_bf_lo(xb);
+    xr[q + 1] = k3_bf_hi(xb);
+    am = __builtin_fmaxf(am, __builtin_fabsf(xr[q]));
+    am = __builtin_fmaxf(am, __builtin_fabsf(xr[q + 1]));
+  }
+  uint32_t mx = __float_as_uint(am) >> 16, my = mx;
+  k3g_swap(mx, my);  // mx: lane l % 32's amax, my: lane 32 + l % 32's
+  const int ex = k3_e8m0_exp(mx > my ? mx : my);
+  const float(&x0)[8] = *reinterpret_cast<const float(*)[8]>(&xr[0]);
+  const float(&x1)[8] = *reinterpret_cast<const float(*)[8]>(&xr[8]);
+  const k3_u2 c0 = k3_f8_to_e4m3(x0, ex), c1 = k3_f8_to_e4m3(x1, ex);
+  // code dwords: columns 4 h + 0..3, 8 + 4 h.., 16 + 4 h.., 24 + 4 h..
+  uint32_t d0 = c0[0], d1 = c0[1], d2 = c1[0], d3 = c1[1];
+  k3g_swap(d0, d2);
+  k3g_swap(d1, d3);
+  k3_st16(o + 16 * h, (k3_u4){d0, d2, d1, d3});
+  return (uint32_t)(ex + 127);
+}
+
 template <int KGM>
 K3_DEV void k3g_gemm_situ_mx(K3G_PARAMS, uint8_t* __restrict__ out_q, uint8_t* __restrict__ out_sf,
                              const float* __restrict__ alpha, const float* __restrict__ beta) {
@@ -531,41 +568,10 @@ K3_DEV void k3g_gemm_situ_mx(K3G_PARAMS, uint8_t* __restrict__ out_q, uint8_t* _
       const size_t row = (size_t)tile * K3G_TILE_M + 64 * wm + 32 * mt + j;
       uint32_t sfp = 0;
 #pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        // bf16 activations in q order, as f32; their block amax in f32 (the max of
-        // bf16 values is a bf16 value, NaN ignored as in kern_k3_moe_quant)
-        float xr[16];
-        float am = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 16; q += 2) {
-          const uint32_t u2 = k3_pack_bf2(acc[mt][2 * p][q], acc[mt][2 * p][q + 1]);
-          const uint32_t g2 = k3_pack_bf2(acc[mt][2 * p + 1][q], acc[mt][2 * p + 1][q + 1]);
-          float x[2];
-#pragma unroll
-          for (int d = 0; d < 2; ++d) {
-            const float u = d ? k3_bf_hi(u2) : k3_bf_lo(u2);
-            const float g = d ? k3_bf_hi(g2) : k3_bf_lo(g2);
-            x[d] = k3c ? k3_situ(g, u) : k3_situ_gate_a(g, al, ial) * k3_situ_up_b(u, be, ibe);
-          }
-          const uint32_t xb = k3_pack_bf2(x[0], x[1]);
-          xr[q] = k3_bf_lo(xb);
-          xr[q + 1] = k3_bf_hi(xb);
-          am = __builtin_fmaxf(am, __builtin_fabsf(xr[q]));
-          am = __builtin_fmaxf(am, __builtin_fabsf(xr[q + 1]));
-        }
-        uint32_t mx = __float_as_uint(am) >> 16, my = mx;
-        k3g_swap(mx, my);  // mx: lane l % 32's amax, my: lane 32 + l % 32's
-        const int ex = k3_e8m0_exp(mx > my ? mx : my);
-        const float(&x0)[8] = *reinterpret_cast<const float(*)[8]>(&xr[0]);
-        const float(&x1)[8] = *reinterpret_cast<const float(*)[8]>(&xr[8]);
-        const k3_u2 c0 = k3_f8_to_e4m3(x0, ex), c1 = k3_f8_to_e4m3(x1, ex);
-        // code dwords: columns 4 h + 0..3, 8 + 4 h.., 16 + 4 h.., 24 + 4 h..
-        uint32_t d0 = c0[0], d1 = c0[1], d2 = c1[0], d3 = c1[1];
-        k3g_swap(d0, d2);
-        k3g_swap(d1, d3);
-        k3_st16(out_q + row * NA + col0 + 32 * p + 16 * h, (k3_u4){d0, d2, d1, d3});
-        sfp |= (uint32_t)(ex + 127) << (8 * p);
-      }
+      for (int p = 0; p < 2; ++p)
+        sfp |= k3g_situ_block(acc[mt][2 * p], acc[mt][2 * p + 1], k3c, al, ial, be, ibe,
+                              out_q + row * NA + col0 + 32 * p, h)
+               << (8 * p);
       if (h == 0) *(uint16_t*)(out_sf + row * (NA / 32) + col0 / 32) = (uint16_t)sfp;
     }
   });
