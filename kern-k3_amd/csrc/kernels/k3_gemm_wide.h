@@ -148,15 +148,18 @@ K3_DEV void k3w_run(const uint8_t* __restrict__ a, const uint8_t* __restrict__ a
   const uint8_t* wsf8 = (const uint8_t*)wsf;
 
   // This lane's source rows of item t: the A-row byte offsets of its two row-slice
-  // loads (rows 8 q + l / 8, q = 2 w, 2 w + 1) and the A-scale byte offset of row
-  // 16 w + l % 16 (every activation row offset fits in 32 bits: rows * K < 2^32).
+  // loads (rows 8 q + l / 8, q = 2 w, 2 w + 1, plus the lane's chunk) and the
+  // A-scale byte offset of row 16 w + l % 16 (every activation row offset fits in
+  // 32 bits: rows * K < 2^32).
   auto rows_of = [&](const K3wItem& t, uint32_t (&ar)[2], uint32_t& sr) {
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      const int r = t.tile * K3G_TILE_M + 8 * (2 * w + b) + (lane >> 3);
+      const int q = 2 * w + b;
+      const int r = t.tile * K3G_TILE_M + 8 * q + (lane >> 3);
       int src = a_rows ? a_rows[r] : r;
       src = src < 0 ? 0 : src;
-      ar[b] = (uint32_t)src * (uint32_t)K;
+      // the row's offset plus that of the 16-byte chunk this lane moves
+      ar[b] = (uint32_t)src * (uint32_t)K + 16u * (uint32_t)((lane & 7) ^ (lane >> 3) ^ (q & 1));
     }
     const int r = t.tile * K3G_TILE_M + 16 * w + (lane & 15);
     int src = a_rows ? a_rows[r] : r;
@@ -167,31 +170,36 @@ K3_DEV void k3w_run(const uint8_t* __restrict__ a, const uint8_t* __restrict__ a
   // slices q = 2 w, 2 w + 1 (lane l: row 8 q + l / 8, the chunk that lands at slot
   // 8 r + l % 8); B blocks 4 w .. 4 w + 3 (tile b / 2, substep b % 2); lanes 0-15:
   // the A scales of rows 16 w + l and 16 bytes of B-scale group w / 2.
+  // Every address is a wave-uniform base (scalar registers; the step moves it)
+  // plus a 32-bit lane offset fixed per item, so that the loads take the
+  // scalar-base form (global_load_lds ... v_off, s[base]) and a step costs no
+  // vector address arithmetic.  The offsets pass through an empty asm statement
+  // at every step (step() below), which keeps the compiler from hoisting 64-bit
+  // widened copies of them out of the step loop (a widened copy costs a 64-bit
+  // add per load and step).
+  uint32_t lo16 = 16u * (uint32_t)lane;
   auto issue = [&](uint8_t* st, const K3wItem& t, const uint32_t (&ar)[2], uint32_t sr, int k) {
+    const uint8_t* ak = a + (size_t)k * K3G_KSTEP;
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const int q = 2 * w + b;
-      const int c = (lane & 7) ^ (lane >> 3) ^ (q & 1);
-      __builtin_amdgcn_global_load_lds(a + ar[b] + k * K3G_KSTEP + 16 * c,
-                                       (k3g_lds_t*)(st + q * 1024), 16, 0, 0);
-    }
+    for (int b = 0; b < 2; ++b)
+      __builtin_amdgcn_global_load_lds(ak + ar[b], (k3g_lds_t*)(st + (2 * w + b) * 1024), 16, 0, 0);
     const uint8_t* wblk = wt + ((size_t)t.e * NT + (size_t)t.cb * (K3W_TILE_N / 32)) * KT * 1024;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       const int blk = 4 * w + b;
-      __builtin_amdgcn_global_load_lds(
-          wblk + ((size_t)(blk >> 1) * KT + 2 * k + (blk & 1)) * 1024 + 16 * lane,
-          (k3g_lds_t*)(st + K3W_A_BYTES + blk * 1024), 16, 0, 0);
+      const uint8_t* wb = wblk + ((size_t)(blk >> 1) * KT + 2 * k + (blk & 1)) * 1024;
+      __builtin_amdgcn_global_load_lds(wb + lo16, (k3g_lds_t*)(st + K3W_A_BYTES + blk * 1024), 16,
+                                       0, 0);
     }
     const uint8_t* sbg =
         wsf8 + (((size_t)t.e * (NT / 4) + (size_t)t.cb * (K3W_TILE_N / 128) + (w >> 1)) * KS + k) *
                    512 +
         256 * (w & 1);
     if (lane < 16) {
-      __builtin_amdgcn_global_load_lds(a_sf + sr + 4 * k,
+      __builtin_amdgcn_global_load_lds(a_sf + (size_t)4 * k + sr,
                                        (k3g_lds_t*)(st + K3W_SA_OFF + 64 * w), 4, 0, 0);
-      __builtin_amdgcn_global_load_lds(sbg + 16 * lane, (k3g_lds_t*)(st + K3W_SB_OFF + 256 * w),
-                                       16, 0, 0);
+      __builtin_amdgcn_global_load_lds(sbg + lo16, (k3g_lds_t*)(st + K3W_SB_OFF + 256 * w), 16, 0,
+                                       0);
     }
   };
 
@@ -223,26 +231,39 @@ K3_DEV void k3w_run(const uint8_t* __restrict__ a, const uint8_t* __restrict__ a
 
   K3wOps op;
   const int r0 = 64 * g + j;  // this lane's row in m tile 0 (m tile 1: + 32)
+  // The lane's A slots: row r0 + 32 mt sits 256 slots (4096 bytes) after row r0
+  // in the same chunk order (the swizzle depends on r % 16 only), so the four
+  // chunks' byte offsets serve both m tiles.
+  int aoff[2][2];  // [substep][low / high chunk]
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    aoff[s][0] = 16 * k3g_aslot(r0, 4 * s + h);
+    aoff[s][1] = 16 * k3g_aslot(r0, 4 * s + 2 + h);
+  }
   auto memory = [&](const uint8_t* st) {
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int s = 0; s < 2; ++s) {
+      const uint8_t* plo = st + aoff[s][0];
+      const uint8_t* phi = st + aoff[s][1];
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const int r = r0 + 32 * mt;
-        const k3_u4 lo = *(const k3_u4*)(st + 16 * k3g_aslot(r, 4 * s + h));
-        const k3_u4 hi = *(const k3_u4*)(st + 16 * k3g_aslot(r, 4 * s + 2 + h));
+      for (int mt = 0; mt < 2; ++mt) {
+        const k3_u4 lo = *(const k3_u4*)(plo + 4096 * mt);
+        const k3_u4 hi = *(const k3_u4*)(phi + 4096 * mt);
         op.av[mt][s] = (k3_v8i){(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
                                 (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
       }
+    }
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
       for (int s = 0; s < 2; ++s)
         op.bv[nt][s] =
             *(const k3_u4*)(st + K3W_A_BYTES + ((4 * wq + nt) * 2 + s) * 1024 + 16 * lane);
+    // A scales: the lane's half-wave byte moved to bytes 0 and 2 (one shift per m
+    // tile), so that the MFMA's scale byte select is a per-instruction constant
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
-      op.sa[mt] = *(const uint32_t*)(st + K3W_SA_OFF + 4 * (r0 + 32 * mt));
+      op.sa[mt] = *(const uint32_t*)(st + K3W_SA_OFF + 4 * (r0 + 32 * mt)) >> (8 * h);
     op.sb = *(const uint2*)(st + K3W_SB_OFF + 512 * wq + 8 * lane);
   };
   // The accumulators pass through empty volatile asm at both edges of a compute
@@ -254,22 +275,27 @@ K3_DEV void k3w_run(const uint8_t* __restrict__ a, const uint8_t* __restrict__ a
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) asm volatile("" : "+v"(acc[mt][nt]));
   };
+  // One substep s of n tile NT for both m tiles.  Scale bytes are picked by the
+  // instruction's byte selects: B block 4 k + 2 s + h of column j is byte
+  // 2 (NT % 2) + s of the tile group's word, A block 4 k + 2 s + h of row j byte
+  // 2 s of the shifted dword.
+  auto mfma2 = [&](auto nt_c, auto s_c) {
+    constexpr int nt = decltype(nt_c)::value, s = decltype(s_c)::value;
+    const k3_u4& b = op.bv[nt][s];
+    const k3_v8i bw = {(int)b[0], (int)b[1], (int)b[2], (int)b[3], 0, 0, 0, 0};
+    const uint32_t sb = nt & 2 ? op.sb.y : op.sb.x;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+      acc[mt][nt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+          bw, op.av[mt][s], acc[mt][nt], 4, 0, 2 * (nt & 1) + s, (int)sb, 2 * s, (int)op.sa[mt]);
+  };
   auto compute = [&]() {
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt) {
-          const k3_u4& b = op.bv[nt][s];
-          const k3_v8i bw = {(int)b[0], (int)b[1], (int)b[2], (int)b[3], 0, 0, 0, 0};
-          // scale bytes: B block 4 k + 2 s + h of column j (byte s of the tile's
-          // pair), A block 4 k + 2 s + h of row j (byte 2 s + h of the dword)
-          const uint32_t sb = (nt & 2 ? op.sb.y : op.sb.x) >> (16 * (nt & 1) + 8 * s);
-          const uint32_t sa = op.sa[mt] >> (16 * s + 8 * h);
-          acc[mt][nt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-              bw, op.av[mt][s], acc[mt][nt], 4, 0, 0, (int)sb, 0, (int)sa);
-        }
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    mfma2(I0{}, I0{}); mfma2(I1{}, I0{}); mfma2(I2{}, I0{}); mfma2(I3{}, I0{});
+    mfma2(I0{}, I1{}); mfma2(I1{}, I1{}); mfma2(I2{}, I1{}); mfma2(I3{}, I1{});
   };
 
   bool more = L.live(nx);
@@ -280,6 +306,8 @@ K3_DEV void k3w_run(const uint8_t* __restrict__ a, const uint8_t* __restrict__ a
   // step landed (those just issued left in flight).
   auto step = [&](int i, int S) {
     __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" : "+v"(arow[0]), "+v"(arow[1]), "+v"(srow), "+v"(lo16));
+    asm volatile("" : "+v"(arow_n[0]), "+v"(arow_n[1]), "+v"(srow_n));
     int nvm = 0;
     const int S2 = S == 0 ? 2 : S - 1;  // (S + 2) % 3
     if (i + 2 < KS) {
