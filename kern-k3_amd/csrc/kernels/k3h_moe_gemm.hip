@@ -190,20 +190,22 @@ K3_DEV uint8_t* k3g_smem() {
 // 8 consecutive rows).
 K3_DEV int k3g_aslot(int r, int c) { return 8 * r + (c ^ ((r & 7) ^ ((r >> 3) & 1))); }
 
+// Addresses are a wave-uniform base (scalar registers; the step moves it) plus a
+// 32-bit lane offset fixed per item, so that the loads take the scalar-base form
+// (global_load_lds ... v_off, s[base]) and a step costs no vector address
+// arithmetic: arow[b] holds the lane's row offset plus its chunk's, lo16 = 16 l.
 K3_DEV void k3g_issue_stage(uint8_t* st, const uint8_t* a, const uint32_t* arow,
-                            const uint8_t* wblk, int ks, int KT, int w, int lane) {
-  const int k0 = ks * K3G_KSTEP;
+                            const uint8_t* wblk, int ks, int KT, int w, uint32_t lo16) {
+  const uint8_t* ak = a + (size_t)ks * K3G_KSTEP;
 #pragma unroll
-  for (int b = 0; b < 4; ++b) {  // rows 32 w + 8 b .. + 8 of the tile (q = 4 w + b)
-    const int c = (lane & 7) ^ (lane >> 3) ^ (b & 1);  // the chunk this lane moves
-    __builtin_amdgcn_global_load_lds(a + arow[b] + k0 + 16 * c,
-                                     (k3g_lds_t*)(st + (4 * w + b) * 1024), 16, 0, 0);
-  }
+  for (int b = 0; b < 4; ++b)  // rows 32 w + 8 b .. + 8 of the tile (q = 4 w + b)
+    __builtin_amdgcn_global_load_lds(ak + arow[b], (k3g_lds_t*)(st + (4 * w + b) * 1024), 16, 0, 0);
 #pragma unroll
   for (int b = 0; b < 4; ++b) {  // B blocks: tiles 2 w, 2 w + 1, both substeps
     const int T = 2 * w + (b >> 1), s = b & 1;
-    __builtin_amdgcn_global_load_lds(wblk + ((size_t)T * KT + 2 * ks + s) * 1024 + 16 * lane,
-                                     (k3g_lds_t*)(st + 16384 + (T * 2 + s) * 1024), 16, 0, 0);
+    const uint8_t* wb = wblk + ((size_t)T * KT + 2 * ks + s) * 1024;
+    __builtin_amdgcn_global_load_lds(wb + lo16, (k3g_lds_t*)(st + 16384 + (T * 2 + s) * 1024), 16,
+                                     0, 0);
   }
 }
 
@@ -223,15 +225,19 @@ K3_DEV void k3g_lds_loop(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
     const int r = tile * K3G_TILE_M + 32 * w + 8 * b + (lane >> 3);
     int src = a_rows ? a_rows[r] : r;
     src = src < 0 ? 0 : src;
-    arow[b] = (uint32_t)src * (uint32_t)K;
+    // the row's offset plus that of the 16-byte chunk this lane moves
+    arow[b] = (uint32_t)src * (uint32_t)K + 16u * (uint32_t)((lane & 7) ^ (lane >> 3) ^ (b & 1));
   }
+  uint32_t lo16 = 16u * (uint32_t)lane;
   const size_t T0 = (size_t)e * NT + cb * (K3G_TILE_N / 32);
   const uint8_t* wblk = wt + T0 * KT * 1024;
   // this wave's B scale pairs: group G = T0 / 4 + wn of its 4 tiles, 8 bytes per lane
-  // per step
-  const uint2* sbp =
-      (const uint2*)wsf + ((size_t)e * (NT / 4) + cb * (K3G_TILE_N / 128) + wn) * KS * 64 +
-      lane;
+  // per step (a wave-uniform base in scalar registers plus the lane's 8 l)
+  const uint8_t* sbu = (const uint8_t*)wsf +
+                       ((size_t)e * (NT / 4) + cb * (K3G_TILE_N / 128) + wn) * KS * 512;
+  asm volatile("" : "+s"(wblk), "+s"(sbu));  // both wave-uniform: scalar registers
+  uint32_t lo8 = 8u * (uint32_t)lane;
+  auto sb_step = [&](int k) -> uint2 { return *(const uint2*)(sbu + (size_t)k * 512 + lo8); };
 
   // the tile's A scales for all of K (KG <= KGM bytes per row), once
   // (two threads per row, each one row lookup and then independent dword loads)
@@ -247,13 +253,13 @@ K3_DEV void k3g_lds_loop(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
 #pragma unroll 8
     for (int d = d0; d < d1; ++d) dr[d] = sr[d];
   }
-  uint2 sbc = sbp[0];                               // B scale pairs of the current step
-  uint2 sbq = KS > 1 ? sbp[64] : make_uint2(0, 0);  // and of the next one
+  uint2 sbc = sb_step(0);                               // B scale pairs of the current step
+  uint2 sbq = KS > 1 ? sb_step(1) : make_uint2(0, 0);  // and of the next one
   __syncthreads();  // no stage load is in flight yet
-  k3g_issue_stage(lds, a, arow, wblk, 0, KT, w, lane);
+  k3g_issue_stage(lds, a, arow, wblk, 0, KT, w, lo16);
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_s_barrier();  // stage 0 landed for every wave
-  if (KS > 1) k3g_issue_stage(lds + K3G_STAGE_BYTES, a, arow, wblk, 1, KT, w, lane);
+  if (KS > 1) k3g_issue_stage(lds + K3G_STAGE_BYTES, a, arow, wblk, 1, KT, w, lo16);
 
   // Operand reads.  The A operand of substep s: row r = 32 (2 wm + mt) + j, chunks
   // 4 s + h and 4 s + 2 + h of its 128-byte slice; the B operand: 1 KB block
@@ -268,18 +274,42 @@ K3_DEV void k3g_lds_loop(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
   auto rd_b = [&](const uint8_t* st, int s, int nt) -> k3_u4 {
     return *(const k3_u4*)(st + 16384 + ((4 * wn + nt) * 2 + s) * 1024 + 16 * lane);
   };
+  // A scales of the step: the lane's half-wave byte shifted to bytes 0 and 2, so
+  // that the MFMA's scale byte select is a per-instruction constant
   auto rd_sa = [&](int ks, int mt) -> uint32_t {
-    return *(const uint32_t*)(sat + (32 * (2 * wm + mt) + j) * K3G_SAT_ROW(KGM) + 4 * ks);
+    return *(const uint32_t*)(sat + (32 * (2 * wm + mt) + j) * K3G_SAT_ROW(KGM) + 4 * ks) >>
+           (8 * h);
   };
-  auto mfma = [&](int mt, int nt, const k3_v8i& av, const k3_u4& bv, uint32_t sa, uint32_t sb,
-                  int s) {
+  // Both m tiles of n tile NT, substep S.  Scale bytes by the instruction's byte
+  // selects: B block 4 k + 2 S + h of column j is byte 2 (NT % 2) + S of the tile
+  // group's word (x: tiles 0, 1; y: tiles 2, 3), A block 4 k + 2 S + h of row j
+  // byte 2 S of the shifted dword.
+  auto mfma2 = [&](auto nt_c, auto s_c, const k3_v8i (&av)[2], const k3_u4& bv,
+                   const uint32_t (&sa2)[2], uint2 sbw) {
+    constexpr int nt = decltype(nt_c)::value, s = decltype(s_c)::value;
+    constexpr int bsel = 2 * (nt & 1) + s, asel = 2 * s;
     const k3_v8i b = {(int)bv[0], (int)bv[1], (int)bv[2], (int)bv[3], 0, 0, 0, 0};
-    if constexpr (SW)  // weights as src0: lane (j, h) accumulates row j, 16 columns
-      acc[mt][nt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-          b, av, acc[mt][nt], 4, 0, 0, (int)(sb >> (8 * s)), 0, (int)(sa >> (16 * s + 8 * h)));
-    else
-      acc[mt][nt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-          av, b, acc[mt][nt], 0, 4, 0, (int)(sa >> (16 * s + 8 * h)), 0, (int)(sb >> (8 * s)));
+    const int sb = (int)(nt & 2 ? sbw.y : sbw.x);
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      if constexpr (SW)  // weights as src0: lane (j, h) accumulates row j, 16 columns
+        acc[mt][nt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+            b, av[mt], acc[mt][nt], 4, 0, bsel, sb, asel, (int)sa2[mt]);
+      else
+        acc[mt][nt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+            av[mt], b, acc[mt][nt], 0, 4, asel, (int)sa2[mt], bsel, sb);
+    }
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  // f(nt) for nt = 0..3 as compile-time constants
+  auto for_nt = [&](auto&& f) {
+    f(I0{});
+    f(I1{});
+    f(I2{});
+    f(I3{});
   };
 
   // Software pipeline: the operands of the next substep are read from LDS behind
@@ -301,21 +331,23 @@ K3_DEV void k3g_lds_loop(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
 
   auto step = [&](int ks, auto more_c, auto issue_c) {
     constexpr bool MORE = decltype(more_c)::value, ISSUE = decltype(issue_c)::value;
+    // the load offsets pass through an empty asm statement at every step, which
+    // keeps the compiler from hoisting 64-bit widened copies of them out of the
+    // loop (a widened copy costs a 64-bit add per load and step)
+    asm volatile("" : "+v"(arow[0]), "+v"(arow[1]), "+v"(arow[2]), "+v"(arow[3]), "+v"(lo16),
+                 "+v"(lo8));
     uint8_t* st = lds + (ks & 1) * K3G_STAGE_BYTES;
     const uint8_t* sn = lds + ((ks + 1) & 1) * K3G_STAGE_BYTES;
-    uint32_t sb[4], san[2];
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
-      sb[nt] = ((nt & 2 ? sbc.y : sbc.x) >> (16 * (nt & 1))) & 0xffffu;
+    uint32_t san[2];
+    const uint2 sbw = sbc;
     // substep 0: A of substep 1 requested first, each B operand re-read behind its pair
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) a1[mt] = rd_a(st, 1, mt);
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      mfma(0, nt, a0[0], bv[nt], sa[0], sb[nt], 0);
-      mfma(1, nt, a0[1], bv[nt], sa[1], sb[nt], 0);
+    for_nt([&](auto nt_c) {
+      constexpr int nt = decltype(nt_c)::value;
+      mfma2(nt_c, I0{}, a0, bv[nt], sa, sbw);
       bv[nt] = rd_b(st, 1, nt);
-    }
+    });
     __builtin_amdgcn_sched_group_barrier(K3G_SG_DS_READ, 4, 0);
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
@@ -326,7 +358,7 @@ K3_DEV void k3g_lds_loop(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
       __builtin_amdgcn_s_waitcnt(0);  // this wave: stage ks + 1 landed, its reads of stage ks done
       __builtin_amdgcn_s_barrier();   // every wave
       sbc = sbq;
-      if constexpr (ISSUE) sbq = sbp[(size_t)(ks + 2) * 64];
+      if constexpr (ISSUE) sbq = sb_step(ks + 2);
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) a0[mt] = rd_a(sn, 0, mt);
 #pragma unroll
@@ -334,14 +366,13 @@ K3_DEV void k3g_lds_loop(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
     }
     // substep 1; the next step's operands are read behind it, and stage ks is
     // refilled with step ks + 2 behind its first MFMA pair
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      mfma(0, nt, a1[0], bv[nt], sa[0], sb[nt], 1);
-      mfma(1, nt, a1[1], bv[nt], sa[1], sb[nt], 1);
+    for_nt([&](auto nt_c) {
+      constexpr int nt = decltype(nt_c)::value;
+      mfma2(nt_c, I1{}, a1, bv[nt], sa, sbw);
       if constexpr (MORE) bv[nt] = rd_b(sn, 0, nt);
       if constexpr (ISSUE)
-        if (nt == 0) k3g_issue_stage(st, a, arow, wblk, ks + 2, KT, w, lane);
-    }
+        if (nt == 0) k3g_issue_stage(st, a, arow, wblk, ks + 2, KT, w, lo16);
+    });
     if constexpr (MORE) {
       sa[0] = san[0];
       sa[1] = san[1];
@@ -407,7 +438,7 @@ K3_DEV bool k3g_block(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
                       int& e, int& lane, int& wm, int& wn) {
   e = cta_batch[tile];
   if (e < 0 || e >= E) return false;
-  const int w = threadIdx.x >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   lane = threadIdx.x & 63;
   wm = w >> 1;
   wn = w & 1;
