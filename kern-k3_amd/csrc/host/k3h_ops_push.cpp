@@ -1,9 +1,10 @@
 // Typed wrappers: the residual push family (res_in with the normed row stored
 // into every TP rank's normed_all, its statistics hand-off to res_mlp, and the
-// land_add2 fold), plus res_mlp's statistics-consuming nb entries.  Grids are
-// the manifest's: one 128-thread workgroup per row, grid ceil_div(tokens, 4) =
-// B rows per rank (k3-tp4-prefill-16k.json:406806 attnres_rms_push_first_v3,
-// 407299 attnres_rms_push_add2, 406999 land_add_attnres_rms_bf16_v2_nb4).
+// land_add2 fold), plus res_mlp's statistics-consuming nb entries.  One
+// workgroup per row, grid ceil_div(tokens, 4) = B rows per rank as the manifest's
+// (k3-tp4-prefill-16k.json:406806 attnres_rms_push_first_v3, 407299
+// attnres_rms_push_add2, 406999 land_add_attnres_rms_bf16_v2_nb4): 128 threads
+// at nb 0 (the manifest entry), 256 threads (the vector-split entries) at nb >= 1.
 #include <string>
 
 #include "k3h_internal.h"

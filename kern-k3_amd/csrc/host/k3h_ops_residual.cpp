@@ -73,8 +73,8 @@ K3H_API int k3h_land_add_attnres_rms_nb(k3h_ctx_t ctx, void* stream, const void*
   if (!k3h_okp(partial, 16) || !k3h_okp(prefix2, 16)) return K3H_EINVAL;
   if (!snapshot && !k3h_okp(prefix, 16)) return K3H_EINVAL;
   if (B == 0) return K3H_OK;
-  // nb <= kSplitNbMax: the 256-thread vector-split entry (same outputs, every
-  // candidate held on chip); above, the manifest's 128-thread entry
+  // nb <= kSplitNbMax (every nb): the 256-thread vector-split entry (the
+  // manifest entry's outputs, every candidate held on chip)
   const bool split = nb <= kSplitNbMax;
   const std::string entry = (split ? "k3h_land_add_attnres_rms_nb" : "kern_k3_land_add_attnres_rms_nb") +
                             std::to_string(nb) + (split ? "s" : "");
