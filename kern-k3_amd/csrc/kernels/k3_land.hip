@@ -60,13 +60,14 @@
 #endif
 
 #define K3_RMS_EPS 1e-5f
-// Eight bf16 gate values and eight bf16 up values -> eight bf16 outputs.
+// Eight bf16 gate values and eight bf16 up values -> eight bf16 outputs.  The
+// landing kernels take the branch form of the SiTU math (k3_situ<false>).
 K3_DEV k3_u4 k3_situ8(k3_u4 g, k3_u4 u) {
   k3_u4 o;
 #pragma unroll
   for (int j = 0; j < 4; ++j)
-    o[j] = k3_pack_bf2(k3_situ(k3_bf_lo(g[j]), k3_bf_lo(u[j])),
-                       k3_situ(k3_bf_hi(g[j]), k3_bf_hi(u[j])));
+    o[j] = k3_pack_bf2(k3_situ<false>(k3_bf_lo(g[j]), k3_bf_lo(u[j])),
+                       k3_situ<false>(k3_bf_hi(g[j]), k3_bf_hi(u[j])));
   return o;
 }
 
@@ -290,7 +291,7 @@ extern "C" __global__ void __launch_bounds__(1024) kern_k3_land_situ(
   for (int i = blockIdx.y * blockDim.x + threadIdx.x; i < n; i += gridDim.y * blockDim.x) {
     const float g = k3_land(p[(size_t)b * 2 * n + i]);
     const float u = k3_land(p[(size_t)b * 2 * n + n + i]);
-    act[(size_t)b * n + i] = (uint16_t)k3_pack_bf2(k3_situ(g, u), 0.0f);
+    act[(size_t)b * n + i] = (uint16_t)k3_pack_bf2(k3_situ<false>(g, u), 0.0f);
   }
 }
 #endif  // K3_LAND_MODULE == 1
@@ -314,7 +315,7 @@ K3_DEV void k3_situ_bf16_body(const uint16_t* __restrict__ p, uint16_t* __restri
   if (b >= rows) return;
   for (int i = blockIdx.y * blockDim.x + threadIdx.x; i < n; i += gridDim.y * blockDim.x)
     act[(size_t)b * n + i] = (uint16_t)k3_pack_bf2(
-        k3_situ(k3_bf(p[(size_t)b * 2 * n + i]), k3_bf(p[(size_t)b * 2 * n + n + i])), 0.0f);
+        k3_situ<false>(k3_bf(p[(size_t)b * 2 * n + i]), k3_bf(p[(size_t)b * 2 * n + n + i])), 0.0f);
 }
 #endif
 
@@ -416,7 +417,8 @@ extern "C" __global__ void __launch_bounds__(512) kern_k3_situ_rms_bf16(
     if (row >= B) break;
     for (int i = tid; i < n; i += 512)
       act[(size_t)row * n + i] = (uint16_t)k3_pack_bf2(
-          k3_situ(k3_bf(sp[(size_t)row * 2 * n + i]), k3_bf(sp[(size_t)row * 2 * n + n + i])), 0.0f);
+          k3_situ<false>(k3_bf(sp[(size_t)row * 2 * n + i]), k3_bf(sp[(size_t)row * 2 * n + n + i])),
+          0.0f);
   }
 }
 #endif  // K3_LAND_MODULE == 4

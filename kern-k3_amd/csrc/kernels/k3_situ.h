@@ -11,6 +11,13 @@
 #define K3_LOG2E 0x1.715476p+0f
 
 // ---------------------------------------------------------------- SiTU math
+// Per-lane select c ? t : f of two values already computed: the conditional
+// operator over expressions is emitted as a branch (the arms' arithmetic sunk
+// into it, under an exec mask when the condition diverges), which runs every
+// activation as its own short dependent sequence; over two named values it is
+// one select (v_cndmask_b32).
+K3_DEV float k3_vsel(bool c, float t, float f) { return c ? t : f; }
+
 // tanh(y) for |y| < 0.25: y + y^3 (-1/3 + y^2 (2/15 + y^2 (-17/315 + y^2 62/2835)));
 // the first omitted term is below 2^-27 |y| there.
 K3_DEV float k3_tanh_series(float y) {
@@ -27,8 +34,14 @@ K3_DEV float k3_tanh_series(float y) {
 //   result = sign(g) s r m,  m = 4 (1 - t),
 // or, for |g| < 1 where 1 - t cancels, m = (1 + t) 4 tanh(|g| / 4) from the odd
 // series x (1 - x^2 / 48 + x^4 / 1920 - 17 x^6 / 1290240) (x = |g|; the first
-// omitted term is below 2^-21 relative).  Branch-free: both m are evaluated and
-// one selected per lane.
+// omitted term is below 2^-21 relative).
+// SEL true: both m are evaluated and one selected per lane (k3_vsel), the form
+// for code that needs the activations' instruction-level parallelism (the fc1
+// epilogue, two waves per SIMD: 7% faster); false: the conditional operator
+// over the two expressions, which the compiler lowers to exec-masked branches
+// (the landing kernels, eight waves per SIMD: measured 15% faster in this form).
+// Both forms compute the same values.
+template <bool SEL = true>
 K3_DEV float k3_situ_gate(float g) {
   const float x = __builtin_fabsf(g);
   const float t = __builtin_amdgcn_exp2f(x * (-0.5f * K3_LOG2E));
@@ -39,7 +52,9 @@ K3_DEV float k3_situ_gate(float g) {
   float p = __builtin_fmaf(x2, -17.0f / 1290240.0f, 1.0f / 1920.0f);
   p = __builtin_fmaf(p, x2, -1.0f / 48.0f);
   p = __builtin_fmaf(p, x2, 1.0f);
-  const float m = x < 1.0f ? p * x * a : __builtin_fmaf(-4.0f, t, 4.0f);
+  float m;
+  if constexpr (SEL) m = k3_vsel(x < 1.0f, p * x * a, __builtin_fmaf(-4.0f, t, 4.0f));
+  else m = x < 1.0f ? p * x * a : __builtin_fmaf(-4.0f, t, 4.0f);
   const float s = g >= 0.0f ? 1.0f : tt;
   return __builtin_copysignf(m * s * r, g);
 }
@@ -47,43 +62,71 @@ K3_DEV float k3_situ_gate(float g) {
 // 25 tanh(u * 0.04) (the reference scales by the f32 constant 0.04f): with
 // x = |u * 0.04| and e = e^(-2 x), 25 (1 - e) / (1 + e), or for x < 0.25 the odd
 // series x (25 - 25 x^2 / 3 + 10 x^4 / 3 - 85 x^6 / 63) (first omitted term
-// below 2^-21 relative).
+// below 2^-21 relative).  EXPF false: the series alone, the same value wherever
+// x < 0.25, for callers that have established that for every active lane
+// (k3_situ_up_series_ok).  SEL as for k3_situ_gate.
+template <bool SEL = true, bool EXPF = true>
 K3_DEV float k3_situ_up(float u) {
   const float y = u * 0.04f;
   const float x = __builtin_fabsf(y);
-  const float e = __builtin_amdgcn_exp2f(x * (-2.0f * K3_LOG2E));
   const float x2 = x * x;
   float p = __builtin_fmaf(x2, -85.0f / 63.0f, 10.0f / 3.0f);
   p = __builtin_fmaf(p, x2, -25.0f / 3.0f);
   p = __builtin_fmaf(p, x2, 25.0f);
-  const float th = x < 0.25f ? p * x
-                             : __builtin_fmaf(-25.0f, e, 25.0f) * __builtin_amdgcn_rcpf(1.0f + e);
+  if constexpr (!EXPF) return __builtin_copysignf(p * x, y);
+  const float e = __builtin_amdgcn_exp2f(x * (-2.0f * K3_LOG2E));
+  float th;
+  if constexpr (SEL)
+    th = k3_vsel(x < 0.25f, p * x,
+                 __builtin_fmaf(-25.0f, e, 25.0f) * __builtin_amdgcn_rcpf(1.0f + e));
+  else
+    th = x < 0.25f ? p * x : __builtin_fmaf(-25.0f, e, 25.0f) * __builtin_amdgcn_rcpf(1.0f + e);
   return __builtin_copysignf(th, y);
 }
 
-K3_DEV float k3_situ(float g, float u) { return k3_situ_gate(g) * k3_situ_up(u); }
+// Wave-uniform: true when every active lane's |u * 0.04| < 0.25 for each u
+// with |u| <= umax (umax: the lane's largest |u|, NaN treated as needing the
+// exponential form; fl(|u| * 0.04) is monotone in |u|), so that k3_situ_up<false>
+// gives every lane's value.
+K3_DEV bool k3_situ_up_series_ok(float umax) {
+  return __builtin_amdgcn_ballot_w64(!(umax * 0.04f < 0.25f)) == 0;
+}
+
+template <bool SEL = true, bool EXPF = true>
+K3_DEV float k3_situ(float g, float u) {
+  return k3_situ_gate<SEL>(g) * k3_situ_up<SEL, EXPF>(u);
+}
 
 // General alpha / beta (per expert).  inv_alpha = 1 / alpha and inv_beta =
-// 1 / beta (correctly rounded); alpha == 4 takes k3_situ_gate.  Every form here
-// is within a few f32 ulp of the exact activation (relative error below 4e-6,
-// checked against double precision over all f32 inputs in [2^-20, 200]); the
-// fc1 epilogue takes k3_situ when alpha == 4 and beta == 25.
+// 1 / beta (correctly rounded); for alpha == 4 callers take k3_situ_gate (the
+// fc1 epilogue chooses per item).  Every form here is within a few f32 ulp of
+// the exact activation (relative error below 4e-6, checked against double
+// precision over all f32 inputs in [2^-20, 200]); the fc1 epilogue takes
+// k3_situ when alpha == 4 and beta == 25.
 K3_DEV float k3_situ_gate_a(float g, float alpha, float inv_alpha) {
-  if (alpha == 4.0f) return k3_situ_gate(g);
   const float x = __builtin_fabsf(g);
   const float y = x * inv_alpha;
   const float e = __builtin_amdgcn_exp2f(y * (-2.0f * K3_LOG2E));
-  const float th = y < 0.25f ? k3_tanh_series(y) : (1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e);
+  const float th =
+      k3_vsel(y < 0.25f, k3_tanh_series(y), (1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e));
   const float t2 = __builtin_amdgcn_exp2f(x * -K3_LOG2E);  // e^-|g|
   const float r = __builtin_amdgcn_rcpf(1.0f + t2);
   const float sg = g >= 0.0f ? r : t2 * r;
   return __builtin_copysignf(alpha * th, g) * sg;
 }
 
+// EXPF false: the series alone (k3_situ_up_b_series_ok), as k3_situ_up.
+template <bool EXPF = true>
 K3_DEV float k3_situ_up_b(float u, float beta, float inv_beta) {
   const float y = u * inv_beta;
   const float x = __builtin_fabsf(y);
+  if constexpr (!EXPF) return beta * __builtin_copysignf(k3_tanh_series(x), y);
   const float e = __builtin_amdgcn_exp2f(x * (-2.0f * K3_LOG2E));
-  const float th = x < 0.25f ? k3_tanh_series(x) : (1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e);
+  const float th =
+      k3_vsel(x < 0.25f, k3_tanh_series(x), (1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e));
   return beta * __builtin_copysignf(th, y);
+}
+
+K3_DEV bool k3_situ_up_b_series_ok(float umax, float inv_beta) {
+  return __builtin_amdgcn_ballot_w64(!(__builtin_fabsf(umax * inv_beta) < 0.25f)) == 0;
 }

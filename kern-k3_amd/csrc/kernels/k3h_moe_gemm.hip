@@ -543,30 +543,50 @@ K3_DEV void k3g_gemm_bf16(K3G_PARAMS, uint16_t* __restrict__ out) {
 // quantised in registers as kern_k3_moe_quant does (block amax of the bf16
 // activations, E8M0 exponent, e4m3 of x * 2^-e), and two exchanges of code
 // dwords leave lane (j, h) with columns 16 h .. + 16 of the block: one 16-byte
-// store per lane and block.  Returns the block's E8M0 byte.
-K3_DEV uint32_t k3g_situ_block(const k3_v16f& up, const k3_v16f& gate, bool k3c, float al,
-                               float ial, float be, float ibe, uint8_t* __restrict__ o, int h) {
+// store per lane and block.  Returns the block's E8M0 byte.  FORM 0: the K3
+// constants (alpha 4, beta 25), k3_situ; 1: alpha 4, general beta; 2: general
+// alpha and beta.  A template parameter, so that the choice is one branch per
+// item rather than one per activation (which would cut the unrolled block into
+// a basic block per activation).
+template <int FORM>
+K3_DEV uint32_t k3g_situ_block(const k3_v16f& up, const k3_v16f& gate, float al, float ial,
+                               float be, float ibe, uint8_t* __restrict__ o, int h) {
   // bf16 activations in q order, as f32; their block amax in f32 (the max of
   // bf16 values is a bf16 value, NaN ignored as in kern_k3_moe_quant)
   float xr[16];
   float am = 0.0f;
+  auto act = [&](auto expf_c) {
+    constexpr bool EXPF = decltype(expf_c)::value;
 #pragma unroll
-  for (int q = 0; q < 16; q += 2) {
-    const uint32_t u2 = k3_pack_bf2(up[q], up[q + 1]);
-    const uint32_t g2 = k3_pack_bf2(gate[q], gate[q + 1]);
-    float x[2];
+    for (int q = 0; q < 16; q += 2) {
+      const uint32_t u2 = k3_pack_bf2(up[q], up[q + 1]);
+      const uint32_t g2 = k3_pack_bf2(gate[q], gate[q + 1]);
+      float x[2];
 #pragma unroll
-    for (int d = 0; d < 2; ++d) {
-      const float u = d ? k3_bf_hi(u2) : k3_bf_lo(u2);
-      const float g = d ? k3_bf_hi(g2) : k3_bf_lo(g2);
-      x[d] = k3c ? k3_situ(g, u) : k3_situ_gate_a(g, al, ial) * k3_situ_up_b(u, be, ibe);
+      for (int d = 0; d < 2; ++d) {
+        const float u = d ? k3_bf_hi(u2) : k3_bf_lo(u2);
+        const float g = d ? k3_bf_hi(g2) : k3_bf_lo(g2);
+        if constexpr (FORM == 0) x[d] = k3_situ<true, EXPF>(g, u);
+        else if constexpr (FORM == 1) x[d] = k3_situ_gate(g) * k3_situ_up_b<EXPF>(u, be, ibe);
+        else x[d] = k3_situ_gate_a(g, al, ial) * k3_situ_up_b<EXPF>(u, be, ibe);
+      }
+      const uint32_t xb = k3_pack_bf2(x[0], x[1]);
+      xr[q] = k3_bf_lo(xb);
+      xr[q + 1] = k3_bf_hi(xb);
+      am = __builtin_fmaxf(am, __builtin_fabsf(xr[q]));
+      am = __builtin_fmaxf(am, __builtin_fabsf(xr[q + 1]));
     }
-    const uint32_t xb = k3_pack_bf2(x[0], x[1]);
-    xr[q] = k3_bf_lo(xb);
-    xr[q + 1] = k3_bf_hi(xb);
-    am = __builtin_fmaxf(am, __builtin_fabsf(xr[q]));
-    am = __builtin_fmaxf(am, __builtin_fabsf(xr[q + 1]));
-  }
+  };
+  // the up factor's exponential form only when some lane of the wave has an up
+  // value past the series range (the bf16 landing is monotone, so the lane's
+  // largest landed |u| is the landing of its largest |u|)
+  float um = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) um = __builtin_fmaxf(um, __builtin_fabsf(up[q]));
+  um = k3_bf_lo(k3_pack_bf2(um, 0.0f));
+  const bool ser = FORM == 0 ? k3_situ_up_series_ok(um) : k3_situ_up_b_series_ok(um, ibe);
+  if (ser) act(std::false_type{});
+  else act(std::true_type{});
   uint32_t mx = __float_as_uint(am) >> 16, my = mx;
   k3g_swap(mx, my);  // mx: lane l % 32's amax, my: lane 32 + l % 32's
   const int ex = k3_e8m0_exp(mx > my ? mx : my);
@@ -591,20 +611,26 @@ K3_DEV void k3g_gemm_situ_mx(K3G_PARAMS, uint8_t* __restrict__ out_q, uint8_t* _
     const float ial = 1.0f / al, ibe = 1.0f / be;
     // the K3 constants (every layer's alpha = 4, beta = 25) take k3_situ, which
     // computes the same values as the general form with fewer instructions
-    const bool k3c = al == 4.0f && be == 25.0f;
+    const int form = al == 4.0f ? (be == 25.0f ? 0 : 1) : 2;
     const int NA = N / 2;                 // activation columns
     const int col0 = 64 * (2 * cb + wn);  // this wave's first activation column
+    auto blocks = [&](auto form_c) {
+      constexpr int FORM = decltype(form_c)::value;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      const size_t row = (size_t)tile * K3G_TILE_M + 64 * wm + 32 * mt + j;
-      uint32_t sfp = 0;
+      for (int mt = 0; mt < 2; ++mt) {
+        const size_t row = (size_t)tile * K3G_TILE_M + 64 * wm + 32 * mt + j;
+        uint32_t sfp = 0;
 #pragma unroll
-      for (int p = 0; p < 2; ++p)
-        sfp |= k3g_situ_block(acc[mt][2 * p], acc[mt][2 * p + 1], k3c, al, ial, be, ibe,
-                              out_q + row * NA + col0 + 32 * p, h)
-               << (8 * p);
-      if (h == 0) *(uint16_t*)(out_sf + row * (NA / 32) + col0 / 32) = (uint16_t)sfp;
-    }
+        for (int p = 0; p < 2; ++p)
+          sfp |= k3g_situ_block<FORM>(acc[mt][2 * p], acc[mt][2 * p + 1], al, ial, be, ibe,
+                                     out_q + row * NA + col0 + 32 * p, h)
+                 << (8 * p);
+        if (h == 0) *(uint16_t*)(out_sf + row * (NA / 32) + col0 / 32) = (uint16_t)sfp;
+      }
+    };
+    if (form == 0) blocks(std::integral_constant<int, 0>{});
+    else if (form == 1) blocks(std::integral_constant<int, 1>{});
+    else blocks(std::integral_constant<int, 2>{});
   });
 }
 
