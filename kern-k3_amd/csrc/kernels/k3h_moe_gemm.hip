@@ -237,7 +237,14 @@ K3_DEV void k3g_lds_loop(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
                        ((size_t)e * (NT / 4) + cb * (K3G_TILE_N / 128) + wn) * KS * 512;
   asm volatile("" : "+s"(wblk), "+s"(sbu));  // both wave-uniform: scalar registers
   uint32_t lo8 = 8u * (uint32_t)lane;
-  auto sb_step = [&](int k) -> uint2 { return *(const uint2*)(sbu + (size_t)k * 512 + lo8); };
+  // through a global-address-space pointer: after the asm statement the compiler
+  // no longer knows where sbu points and would emit a flat load, which counts on
+  // lgkmcnt as well as vmcnt, so that every wait for an LDS operand read would
+  // also wait for this load (measured: 7% of fc1)
+  typedef const __attribute__((address_space(1))) uint8_t k3g_gu8;
+  auto sb_step = [&](int k) -> uint2 {
+    return *(const uint2*)((k3g_gu8*)sbu + (size_t)k * 512 + lo8);
+  };
 
   // the tile's A scales for all of K (KG <= KGM bytes per row), once
   // (two threads per row, each one row lookup and then independent dword loads)
@@ -355,8 +362,17 @@ K3_DEV void k3g_lds_loop(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
       __builtin_amdgcn_sched_group_barrier(K3G_SG_DS_READ, 1, 0);
     }
     if constexpr (MORE) {
+      // substep 0's MFMAs stay ahead of the wait (without this the compiler sinks
+      // six of the eight past the barrier, which halves the loads' lead)
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) asm volatile("" : "+v"(acc[mt][nt]));
       __builtin_amdgcn_s_waitcnt(0);  // this wave: stage ks + 1 landed, its reads of stage ks done
       __builtin_amdgcn_s_barrier();   // every wave
+      // the copy of the landed scale pair stays behind the wait (hoisted above it,
+      // it takes a wait of its own for every load in flight, the stage's included)
+      asm volatile("" : "+v"(sbq));
       sbc = sbq;
       if constexpr (ISSUE) sbq = sb_step(ks + 2);
 #pragma unroll
