@@ -386,8 +386,17 @@ K3_DEV void k3g_lds_loop(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
       constexpr int nt = decltype(nt_c)::value;
       mfma2(nt_c, I1{}, a1, bv[nt], sa, sbw);
       if constexpr (MORE) bv[nt] = rd_b(sn, 0, nt);
-      if constexpr (ISSUE)
-        if (nt == 0) k3g_issue_stage(st, a, arow, wblk, ks + 2, KT, w, lo16);
+      if constexpr (ISSUE && nt == 0) {
+        // the first pair goes ahead of the loads, and the loads ahead of the rest
+        // (left to itself the scheduler issues them after the third pair, a
+        // shorter lead for the loads)
+        asm volatile("" : "+v"(acc[0][0]), "+v"(acc[1][0]));
+        k3g_issue_stage(st, a, arow, wblk, ks + 2, KT, w, lo16);
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int n = 1; n < 4; ++n) asm volatile("" : "+v"(acc[mt][n]));
+      }
     });
     if constexpr (MORE) {
       sa[0] = san[0];
