@@ -165,6 +165,7 @@ extern "C" __global__ void __launch_bounds__(256) kern_k3h_moe_sf_tile(
 static_assert(K3G_STAGES == 2, "the main loop alternates two stages");
 
 typedef __attribute__((address_space(3))) void k3g_lds_t;
+typedef const __attribute__((address_space(1))) uint8_t k3g_gu8;  // global memory bytes
 #define K3G_SAT_ROW(KGM) ((KGM) + 4)  // A-scale table row stride (bytes)
 
 // The workgroup's LDS: the operand stages of the main loop, then the epilogue's
@@ -203,9 +204,15 @@ K3_DEV void k3g_issue_stage(uint8_t* st, const uint8_t* a, const uint32_t* arow,
 #pragma unroll
   for (int b = 0; b < 4; ++b) {  // B blocks: tiles 2 w, 2 w + 1, both substeps
     const int T = 2 * w + (b >> 1), s = b & 1;
+    // the block's address held in scalar registers and the lane's offset added
+    // last, so that the load takes the scalar-base form (left to itself the
+    // compiler adds the lane offset first and the block offset to a 64-bit vector
+    // address per load); then through a global-address-space pointer, which the
+    // asm statement would otherwise hide
     const uint8_t* wb = wblk + ((size_t)T * KT + 2 * ks + s) * 1024;
-    __builtin_amdgcn_global_load_lds(wb + lo16, (k3g_lds_t*)(st + 16384 + (T * 2 + s) * 1024), 16,
-                                     0, 0);
+    asm volatile("" : "+s"(wb));
+    __builtin_amdgcn_global_load_lds((const k3g_gu8*)wb + lo16,
+                                     (k3g_lds_t*)(st + 16384 + (T * 2 + s) * 1024), 16, 0, 0);
   }
 }
 
@@ -235,13 +242,12 @@ K3_DEV void k3g_lds_loop(k3_v16f (&acc)[2][4], const uint8_t* __restrict__ a,
   // per step (a wave-uniform base in scalar registers plus the lane's 8 l)
   const uint8_t* sbu = (const uint8_t*)wsf +
                        ((size_t)e * (NT / 4) + cb * (K3G_TILE_N / 128) + wn) * KS * 512;
-  asm volatile("" : "+s"(wblk), "+s"(sbu));  // both wave-uniform: scalar registers
+  asm volatile("" : "+s"(sbu));  // wave-uniform: scalar registers
   uint32_t lo8 = 8u * (uint32_t)lane;
   // through a global-address-space pointer: after the asm statement the compiler
   // no longer knows where sbu points and would emit a flat load, which counts on
   // lgkmcnt as well as vmcnt, so that every wait for an LDS operand read would
   // also wait for this load (measured: 7% of fc1)
-  typedef const __attribute__((address_space(1))) uint8_t k3g_gu8;
   auto sb_step = [&](int k) -> uint2 {
     return *(const uint2*)((k3g_gu8*)sbu + (size_t)k * 512 + lo8);
   };
