@@ -597,7 +597,7 @@ K3_DEV uint32_t k3g_situ_block(const k3_v16f& up, const k3_v16f& gate, float al,
       for (int d = 0; d < 2; ++d) {
         const float u = d ? k3_bf_hi(u2) : k3_bf_lo(u2);
         const float g = d ? k3_bf_hi(g2) : k3_bf_lo(g2);
-        if constexpr (FORM == 0) x[d] = k3_situ<true, EXPF>(g, u);
+        if constexpr (FORM == 0) x[d] = k3_situ_fused<EXPF>(g, u);
         else if constexpr (FORM == 1) x[d] = k3_situ_gate(g) * k3_situ_up_b<EXPF>(u, be, ibe);
         else x[d] = k3_situ_gate_a(g, al, ial) * k3_situ_up_b<EXPF>(u, be, ibe);
       }
