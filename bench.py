@@ -306,7 +306,7 @@ def bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0) -> 
     rs = torch.full((1,), 2.5, dtype=torch.bfloat16, device="cuda")
     idx = torch.empty((T, 8), dtype=torch.int32, device="cuda")
     wts = torch.empty((T, 8), dtype=torch.float32, device="cuda")
-    add("router top-8 (cfg 5a)", "k3h_router_topk_rows", f"[{T},224]", T * 224 * 4 + 896 + 2 * T * 8 * 4,
+    add("router top-8 (cfg 5a)", "k3h_router_topk_pairs", f"[{T},224]", T * 224 * 4 + 896 + 2 * T * 8 * 4,
         timed(lambda: ctx.router_topk(Sx, bias, rs, idx, wts, T, topk=8, stream=s)),
         "latency-bound (sequential picks)",
         cpu=O and (lambda a=(h(Sx), h(bias), int(h(rs)[0])): O.router_topk(a[0], a[1], a[2], T, 8)))
@@ -662,7 +662,7 @@ OP_KERNELS = {
     "KDA output gate (cfg 3b, eps 1e-6)": ["kern_k3_kda_out_gate"],
     "MLA prep (cfg 4, reference form)": ["k3h_mla_prep_fused"],
     "MLA latent norm + RoPE + q pack": ["k3h_mla_rope_pack"],
-    "router top-8 (cfg 5a)": ["k3h_router_topk_rows"],
+    "router top-8 (cfg 5a)": ["k3h_router_topk_pairs"],
     "EP routing tables (count+tables+scatter)": ["kern_k3_moe_route_count", "kern_k3_moe_route_tables",
                                                  "kern_k3_moe_route_scatter"],
     "EP routing, one launch (k3h_moe_route)": ["k3h_moe_route_fused"],

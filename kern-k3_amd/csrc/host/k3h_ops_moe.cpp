@@ -36,8 +36,9 @@ K3H_API int k3h_router_topk(k3h_ctx_t ctx, void* stream, int topk, const float* 
     return K3H_EINVAL;
   K3hArgs a;
   a.ptr(S).ptr(bias).ptr(rs).ptr(idx).ptr(wts).i32(B);
-  // one row per wave (the manifest entry kern_k3_router_topk idles three waves of four)
-  return k3h_run(ctx, key.c_str(), "k3h_router_topk_rows", k3h_cdiv(B, 4), 1, 1, 256, stream, a);
+  // one row per half-wave (the manifest entry kern_k3_router_topk idles three waves of four
+  // and gives the live one a row alone)
+  return k3h_run(ctx, key.c_str(), "k3h_router_topk_pairs", k3h_cdiv(B, 8), 1, 1, 256, stream, a);
 }
 
 K3H_API int k3h_argmax_f32(k3h_ctx_t ctx, void* stream, const float* logits, float* pmax,

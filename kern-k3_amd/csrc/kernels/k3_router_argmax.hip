@@ -1,7 +1,7 @@
 // Module k3_router_argmax[+TOPK=n]: MoE router top-k and the two-stage f32 argmax.
 //
 //   kern_k3_router_topk(S, bias, rs, idx, wts, B)      grid (B), block 256
-//   k3h_router_topk_rows(S, bias, rs, idx, wts, B)     grid ceil(B / 4), block 256
+//   k3h_router_topk_pairs(S, bias, rs, idx, wts, B)    grid ceil(B / 8), block 256
 //   kern_k3_argmax_f32_partial(logits, pmax, pidx, n)  grid (B, PARTS), block 1024
 //   kern_k3_argmax_f32_final(pmax, pidx, out, parts)   grid (B), block 64
 //
@@ -20,7 +20,8 @@
 // are reproduced bit for bit by the CPU checker.  One wave does the row:
 // expert e = lane + 64 j lives in slot j of lane `lane`.  In the manifest
 // geometry the other three waves of the 256-thread block have no work;
-// k3h_router_topk_rows (no reference counterpart) gives each wave a row.
+// k3h_router_topk_pairs (no reference counterpart, below) gives each half-wave
+// a row.
 #include "../common/k3_dev.h"
 
 #define EXPERTS 224
@@ -143,13 +144,118 @@ extern "C" __global__ void __launch_bounds__(256) kern_k3_router_topk(
   k3_router_row(S, bias, rs, idx, wts, b, threadIdx.x);
 }
 
-// Same contract, one row per wave: grid ceil(B / 4), block 256.
-extern "C" __global__ void __launch_bounds__(256) k3h_router_topk_rows(
+
+// ---------------------------------------------------------------- two rows per wave
+// The same contract with one row per half-wave (k3h_router_topk_pairs, no
+// reference counterpart): grid ceil(B / 8), block 256.  Expert e = s + 32 j
+// (s = lane % 32, j < 7) lives in slot j of lane s of its half; each lane keeps
+// its seven (key, slot) sorted (a 16-comparator network: largest key first, ties
+// to the smaller slot, which is the smaller expert id), so a pick is a max over
+// the half's heads and one ballot, and the two rows share every instruction of
+// the pick loop.  When several heads of a half hold its maximum (rare) a second
+// max over 255 - e picks the smallest expert id, as in k3_router_row.
+#define PSLOTS (EXPERTS / 32)  // 7 slots per lane
+static_assert(EXPERTS % 32 == 0, "whole slots per half-wave");
+
+// Largest value over the lane's half-wave, on every lane of it: four DPP steps
+// give each 16-lane row its maximum, then v_permlane16_swap exchanges the
+// half's two rows (rows 2k and 2k + 1; with both operands the same value, the
+// two results hold the lane's own row and the other row of its pair).
+K3_DEV uint32_t k3_router_half_max(uint32_t v) {
+  uint32_t o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, K3_DPP_QP_1032, 0xf, 0xf, true);
+  v = v > o ? v : o;
+  o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, K3_DPP_QP_2301, 0xf, 0xf, true);
+  v = v > o ? v : o;
+  o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, K3_DPP_ROW_HALF_MIRROR, 0xf, 0xf, true);
+  v = v > o ? v : o;
+  o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, K3_DPP_ROW_MIRROR, 0xf, 0xf, true);
+  v = v > o ? v : o;
+  const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return r[0] > r[1] ? r[0] : r[1];
+}
+
+extern "C" __global__ void __launch_bounds__(256) k3h_router_topk_pairs(
     const float* __restrict__ S, const float* __restrict__ bias, const uint16_t* __restrict__ rs,
     int* __restrict__ idx, float* __restrict__ wts, int B) {
-  const int b = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
-  if (b >= B) return;
-  k3_router_row(S, bias, rs, idx, wts, b, threadIdx.x & 63);
+  const int lane = threadIdx.x & 63, s = lane & 31, h = lane >> 5;
+  const int b0 = 2 * (int)(blockIdx.x * 4 + (threadIdx.x >> 6));  // the wave's first row
+  if (b0 >= B) return;                                              // whole wave
+  const int b = b0 + h;
+  const bool live = b < B;  // the second half of the last wave may have no row
+  const float* row = S + (size_t)(live ? b : B - 1) * EXPERTS;
+
+  float sv_[PSLOTS], bv_[PSLOTS];
+#pragma unroll
+  for (int j = 0; j < PSLOTS; ++j) {
+    sv_[j] = row[s + 32 * j];
+    bv_[j] = bias[s + 32 * j];
+  }
+  float sig[PSLOTS];
+  uint32_t hk[PSLOTS];
+  int jj[PSLOTS];
+#pragma unroll
+  for (int j = 0; j < PSLOTS; ++j) {
+    sig[j] = k3_sigmoid_nb(sv_[j]);
+    hk[j] = k3_ord_f32(sig[j] + bv_[j]);
+    jj[j] = j;
+  }
+  auto cswap = [&](int x, int y) {  // order positions x < y (no short circuit: one select each)
+    const bool sw = (hk[x] < hk[y]) | ((hk[x] == hk[y]) & (jj[x] > jj[y]));
+    const uint32_t kx = hk[x], ky = hk[y];
+    const int jx = jj[x], jy = jj[y];
+    hk[x] = sw ? ky : kx; hk[y] = sw ? kx : ky;
+    jj[x] = sw ? jy : jx; jj[y] = sw ? jx : jy;
+  };
+  static_assert(PSLOTS == 7, "the network sorts seven slots");
+  cswap(0, 6); cswap(2, 3); cswap(4, 5);
+  cswap(0, 2); cswap(1, 4); cswap(3, 6);
+  cswap(0, 1); cswap(2, 5); cswap(3, 4);
+  cswap(1, 2); cswap(4, 6);
+  cswap(2, 3); cswap(4, 5);
+  cswap(1, 2); cswap(3, 4); cswap(5, 6);
+
+  int my_lw = 0, my_jw = 0;
+  for (int r = 0; r < TOPK; ++r) {
+    const uint32_t m = k3_router_half_max(hk[0]);
+    const unsigned long long mk = __ballot(hk[0] == m);
+    const uint32_t m0 = (uint32_t)mk, m1 = (uint32_t)(mk >> 32);
+    int lw0, lw1;
+    if (__builtin_popcount(m0) == 1 && __builtin_popcount(m1) == 1) {
+      lw0 = __builtin_ctz(m0);
+      lw1 = __builtin_ctz(m1);
+    } else {
+      const uint32_t cand = hk[0] == m ? 255u - (uint32_t)(32 * jj[0] + s) : 0u;
+      const uint32_t cm = k3_router_half_max(cand);
+      lw0 = (int)((255u - (uint32_t)__builtin_amdgcn_readlane((int)cm, 0)) & 31u);
+      lw1 = (int)((255u - (uint32_t)__builtin_amdgcn_readlane((int)cm, 32)) & 31u);
+    }
+    const int jw0 = __builtin_amdgcn_readlane(jj[0], lw0);
+    const int jw1 = __builtin_amdgcn_readlane(jj[0], 32 + lw1);
+    const int lw = h ? lw1 : lw0, jw = h ? jw1 : jw0;
+    if (s == lw) {
+#pragma unroll
+      for (int j = 0; j + 1 < PSLOTS; ++j) { hk[j] = hk[j + 1]; jj[j] = jj[j + 1]; }
+      hk[PSLOTS - 1] = 0u;
+    }
+    if (s == r) { my_lw = lw; my_jw = jw; }
+  }
+  // pick r's sigmoid: slot my_jw of lane 32 h + my_lw
+  float my_sig = 0.0f;
+#pragma unroll
+  for (int j = 0; j < PSLOTS; ++j) {
+    const float t = __shfl(sig[j], 32 * h + my_lw, 64);
+    my_sig = my_jw == j ? t : my_sig;
+  }
+  const int my_idx = 32 * my_jw + my_lw;
+  // renormalise over the TOPK pick lanes of the half: the butterfly of k3_router_row
+  float den = my_sig;
+#pragma unroll
+  for (int o = TOPK / 2; o > 0; o >>= 1) den += __shfl_xor(den, o, 64);
+  if (live && s < TOPK) {
+    const float rsf = k3_bf(rs[0]);
+    wts[(size_t)b * TOPK + s] = (my_sig / (den + 1e-20f)) * rsf;
+    idx[(size_t)b * TOPK + s] = my_idx;
+  }
 }
 
 // ---------------------------------------------------------------- argmax
