@@ -6,7 +6,8 @@
 //   bf16 -> f32 widening is a shift; f32 -> bf16 is the gfx950 instruction
 //   v_cvt_pk_bf16_f32 (round to nearest even, two values per instruction).
 // * e4m3 payloads are OCP FP8 E4M3 ("fn": no infinities, 0x7f/0xff = NaN,
-//   largest finite 448) produced by v_cvt_pk_fp8_f32 (round to nearest even).
+//   largest finite 448) produced by v_cvt_pk_fp8_f32 (round to nearest even),
+//   with every NaN code made the canonical 0x7f of the saturating conversion.
 // * Every module is compiled with -ffp-contract=off: a fused multiply-add
 //   appears only where it is written as __builtin_fmaf, so the CPU checker
 //   can reproduce each sum bit for bit.
@@ -50,15 +51,24 @@ K3_DEV uint32_t k3_mul_bf2(uint32_t a, uint32_t g) {
 }
 
 // ---------------------------------------------------------------- e4m3
+// NaN codes of a word of four e4m3 bytes made canonical: v_cvt_pk_fp8_f32
+// turns a NaN input into 0xff whatever its sign, the saturating conversion of
+// the reference kernels (__nv_cvt_float_to_fp8 with __NV_SATFINITE) into 0x7f.
+// A byte is NaN exactly when its low seven bits are all ones; adding 1 to those
+// seven bits carries into bit 7 only then (never into the next byte), and that
+// carry clears the byte's sign bit.
+K3_DEV uint32_t k3_e4m3_nan_canon(uint32_t w) {
+  return w & ~(((w & 0x7f7f7f7fu) + 0x01010101u) & 0x80808080u);
+}
 // Two f32 -> two e4m3 bytes in the low half of the result (byte 0 = a).
 K3_DEV uint32_t k3_pack_e4m3x2(float a, float b) {
-  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xffffu;
+  return k3_e4m3_nan_canon((uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xffffu);
 }
 // Four f32 -> one word of four e4m3 bytes (byte k = value k).
 K3_DEV uint32_t k3_pack_e4m3x4(float a, float b, float c, float d) {
   int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
   w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
-  return (uint32_t)w;
+  return k3_e4m3_nan_canon((uint32_t)w);
 }
 
 // E8M0 block exponent of a block whose largest |value| has the bf16 bit

@@ -340,9 +340,19 @@ int k3o_mx_exp(float amax) {
   return e;
 }
 
+/* max(a, b) ignoring a NaN operand, signalling NaN included: the reference's
+ * fmaxf (PTX max.f32) returns the other operand for any NaN, where glibc's
+ * fmaxf follows IEEE 754-2008 maxNum and turns a signalling NaN (a bf16 NaN
+ * pattern with bit 6 clear widens to one) into a quiet NaN result. */
+static float max_nonan(float a, float b) {
+  if (isnan(b)) return a;
+  if (isnan(a)) return b;
+  return b > a ? b : a;
+}
+
 static void mx_block(const float* v, uint8_t* q, uint8_t* sf) {
   float amax = 0.0f;
-  for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j])); /* fmaxf drops NaN */
+  for (int j = 0; j < 32; ++j) amax = max_nonan(amax, fabsf(v[j]));
   const int e = k3o_mx_exp(amax);
   const float s = ldexpf(1.0f, -e); /* exp2f(-e): an exact power of two */
   *sf = (uint8_t)(e + 127);
@@ -402,7 +412,7 @@ void k3o_quant_fp8_amax(const uint16_t* x, int n, float* partials, int nb_grid, 
       float m = 0.0f;
       for (int t = 0; t < 256; ++t)
         for (long long i = (long long)b * 256 + t; i < n; i += stride)
-          m = fmaxf(m, fabsf(k3o_bf2f(x[i])));
+          m = max_nonan(m, fabsf(k3o_bf2f(x[i])));
       partials[b] = m;
     } else {
       uint32_t m = 0;
@@ -429,7 +439,7 @@ void k3o_quant_fp8_amax(const uint16_t* x, int n, float* partials, int nb_grid, 
 void k3o_quant_fp8_apply(const uint16_t* x, uint8_t* y, int n, const float* partials, int nb,
                          float* scale_out) {
   float amax = 0.0f;
-  for (int b = 0; b < nb; ++b) amax = fmaxf(amax, partials[b]);
+  for (int b = 0; b < nb; ++b) amax = max_nonan(amax, partials[b]);
   const float scale = amax > 0.0f ? amax / 448.0f : 1.0f;
   if (scale_out) *scale_out = scale;
   const float inv = 1.0f / scale;

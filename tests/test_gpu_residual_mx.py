@@ -155,14 +155,13 @@ def test_moe_quant(ctx, rows, cols):
 
 
 def test_moe_quant_every_bf16_pattern(ctx):
-    """All 65536 bf16 patterns (NaN excluded) in shuffled 32-value blocks, plus
-    blocks holding +-inf: exercises the hardware e4m3 conversion over every
-    input and many block scales."""
+    """All 65536 bf16 patterns, NaN included, in shuffled 32-value blocks (so
+    blocks also hold +-inf and NaN): exercises the hardware e4m3 conversion over
+    every input and many block scales; NaN inputs give the canonical 0x7f of the
+    saturating conversion and are ignored by the block amax."""
     _case("moe_quant all bf16 patterns")
     g = rng(700)
     h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
-    f = bf16_to_f32(h)
-    h = h[~np.isnan(f)]
     reps = []
     for k in range(4):
         reps.append(h[g.permutation(h.size)])
@@ -184,6 +183,30 @@ def _fused(ctx, x, res, gamma, B, eps, want_normed=True):
     ctx.residual_rms_mxfp8(xd, rd, gd, ro, q, sf, nrm, eps=eps, B=B)
     torch.cuda.synchronize()
     return from_dev(ro), from_dev(q), from_dev(sf), (from_dev(nrm) if want_normed else None)
+
+
+def test_fused_residual_rms_mxfp8_nan(ctx):
+    """NaN in a row (either input, either sign): its residual_out holds the NaN,
+    its whole normed row is NaN, every payload byte the canonical 0x7f and every
+    block scale 127 (the block amax ignores NaN); the other rows are unaffected."""
+    _case("fused residual+rms+mxfp8 NaN rows")
+    B = 4
+    g = rng(850)
+    x = normal_bf16(g, (B, H), outlier_p=0.001)
+    res = normal_bf16(g, (B, H))
+    gamma = normal_bf16(g, (H,), 1.0, 0.1)
+    x[1, 100] = 0x7FC0
+    res[2, 7000] = 0xFFC1
+    x[3, 31] = 0xFF81
+    wro, wq, wsf, wn = O.residual_rms_mxfp8(x, res, gamma, B, 1e-6)
+    ro, q, sf, nrm = _fused(ctx, x, res, gamma, B, 1e-6)
+    _eq("q", q, wq)
+    _eq("sf", sf, wsf)
+    for name, got, want in (("residual_out", ro, wro), ("normed", nrm, wn)):
+        gn, wn_ = np.isnan(bf16_to_f32(got)), np.isnan(bf16_to_f32(want))
+        assert np.array_equal(gn, wn_), f"{name}: NaN positions differ"
+        _eq(name, got[~gn], want[~wn_])
+    assert (q[1:] == 0x7F).all() and (sf[1:] == 127).all() and (q[0] != 0x7F).all()
 
 
 @pytest.mark.parametrize("B", [1024, 16384])

@@ -151,6 +151,38 @@ def test_moe_quant_all_bf16_patterns():
     assert np.array_equal(q.reshape(-1), wq)
 
 
+def test_moe_quant_nan_ignored_by_amax():
+    """A NaN of any kind (quiet or signalling bf16 pattern, either sign, first,
+    middle or last in its block) is ignored by the block amax and quantises to
+    the canonical 0x7f: the block equals the same block with its NaNs replaced
+    by zero everywhere else.  (glibc's fmaxf would turn a signalling NaN into a
+    quiet NaN amax, so a NaN last in its block would reset the scale.)"""
+    g = rng(41)
+    rows, cols = 8, 256
+    x = normal_bf16(g, (rows, cols), outlier_p=0.01)
+    nan_pats = [0x7F81, 0xFF86, 0x7FC0, 0xFFC1, 0x7FFF, 0xFFBF]
+    pos = []
+    for k, pat in enumerate(nan_pats):
+        for j in (0, 17, 31):
+            r, c = (k + j) % rows, 32 * ((k * 3 + j) % (cols // 32)) + j
+            x[r, c] = pat
+            pos.append((r, c))
+    x[7, 64:96] = 0x7F81  # a block of NaN only: amax 0, scale 127
+    z = x.copy()
+    isn = np.isnan(bf16_to_f32(x))
+    z[isn] = 0
+    q, sf = O.moe_quant(x, rows, cols)
+    wq, wsf = _mx_numpy(z)
+    assert np.array_equal(sf.reshape(-1), wsf)
+    assert (q[isn] == 0x7F).all()
+    assert np.array_equal(q[~isn], wq.reshape(rows, cols)[~isn])
+    assert sf[7, 2] == 127
+    # per-tensor v1 partials ignore every NaN as well
+    p = O.quant_fp8_amax(x.reshape(-1), rows * cols, 4, v2=False)
+    pz = O.quant_fp8_amax(z.reshape(-1), rows * cols, 4, v2=False)
+    assert np.array_equal(p, pz)
+
+
 def test_fused_is_k1b_then_moe_quant():
     g = rng(50)
     B = 16
