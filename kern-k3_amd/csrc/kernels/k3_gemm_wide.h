@@ -10,7 +10,7 @@
 // 512-thread workgroup (8 waves, two per SIMD) per CU, grid a multiple of 8;
 // workgroup i serves XCD i % 8 (workgroups are dispatched round-robin over the
 // XCDs) and takes every (grid / 8)-th item of that XCD's part of the items (the
-// XCDs split the live tiles, each taking all column blocks of its tiles),
+// XCDs split the tile-major item list into eight equal contiguous ranges),
 // skipping tiles whose expert is out of range.  Per K step of 128 the
 // workgroup brings 48 KB of operands into LDS (16 KB of A rows, 32 KB of B
 // tiles), 25% fewer bytes per FLOP than the 128 x 256 items of the 4-wave
@@ -89,17 +89,23 @@ struct K3wItem {
 };
 
 // This workgroup's share of the items: slots c, c + ncu, ... below nslots of
-// its XCD's tiles [t0, t0 + nslots / nc) x every column block, tile-major.
+// its XCD's item range [i0, i0 + nslots).  Items are numbered tile-major over
+// the live tiles (item = tile * nc + column block) and the eight XCDs take
+// equal contiguous ranges of them, so no CU has more than ceil(items / 8 / ncu)
+// items whatever the live tile count (a split by whole tiles adds a round
+// whenever the remainder tiles' column blocks overflow it: 290 live tiles, 7
+// column blocks, 32 CUs per XCD gave 9 items to some CUs instead of 8); a tile
+// at a range boundary has its column blocks on two XCDs.
 struct K3wList {
-  int t0, nc, nslots, c, ncu, E;
+  int i0, nc, nslots, c, ncu, E;
   const int* cta_batch;
   // the first item at slot >= s (s = c + k ncu) whose expert is in range;
   // slot >= nslots: none
   K3_DEV K3wItem at(int s) const {
     for (; s < nslots; s += ncu) {
-      const int ti = s / nc;
-      const int tile = t0 + ti, e = cta_batch[tile];
-      if (e >= 0 && e < E) return {s, tile, s - ti * nc, e};
+      const int item = i0 + s;
+      const int tile = item / nc, e = cta_batch[tile];
+      if (e >= 0 && e < E) return {s, tile, item - tile * nc, e};
     }
     return {nslots, 0, 0, 0};
   }
@@ -111,9 +117,9 @@ K3_DEV K3wList k3w_list(const int* __restrict__ num_tiles, const int* __restrict
   int live = *num_tiles;
   live = live < max_tiles ? live : max_tiles;
   const int x = blockIdx.x % K3G_XCDS, ncu = gridDim.x / K3G_XCDS;
-  const int tq = live / K3G_XCDS, tr = live % K3G_XCDS;
-  const int ntx = tq + (x < tr ? 1 : 0), t0 = x * tq + (x < tr ? x : tr);
-  return {t0, nc, ntx * nc, (int)blockIdx.x / K3G_XCDS, ncu, E, cta_batch};
+  const long long total = (long long)live * nc;
+  const int i0 = (int)(total * x / K3G_XCDS), i1 = (int)(total * (x + 1) / K3G_XCDS);
+  return {i0, nc, i1 - i0, (int)blockIdx.x / K3G_XCDS, ncu, E, cta_batch};
 }
 
 struct K3wOps {
