@@ -39,6 +39,7 @@ extern "C" {
 #define K3H_ENOMODULE (-2) /* code object missing or not loadable */
 #define K3H_ENOENTRY (-3)  /* entry name not in the module */
 #define K3H_ENOMEM (-4)
+#define K3H_ERESIDENT (-5) /* the device cannot hold a grid-synchronised launch at once */
 #define K3H_EHIP_BASE (-1000)
 
 typedef struct k3h_module_s* k3h_module_t;
@@ -239,10 +240,15 @@ K3H_API int k3h_moe_route_scatter(k3h_ctx_t ctx, void* stream, int topk, const i
  * ceil(T / 256) <= 256, i.e. T <= 65536, block 512), whose workgroups meet at
  * one grid barrier.  sync: 2 ints of device memory, zero before the first call;
  * each call leaves them zero again.  Calls that share `sync` must not overlap
- * (stream-order them).  The barrier's wait is bounded: if it expires (only
- * possible when the grid cannot be resident at once) total_padded is -1 and
- * the other outputs are incomplete.  T = 0 writes num_non_exiting =
- * total_padded = 0. */
+ * (stream-order them).  Before launching, the call checks that the device holds
+ * the whole grid at once (occupancy x CUs, cached per context and device) and
+ * returns K3H_ERESIDENT otherwise.  The barrier's wait is still bounded and
+ * all-or-nothing: if it expires (some workgroup never became resident) no
+ * workgroup proceeds, num_non_exiting = 0, total_padded = -1 and every
+ * exp2perm entry is -1 (nothing routed: the GEMMs and the permute see no tile,
+ * finalize no local slot); blockoff, cta_batch, cta_limit and route_map are
+ * then not written, and `sync` still comes back zero.  T = 0 writes
+ * num_non_exiting = total_padded = 0. */
 K3H_API int k3h_moe_route(k3h_ctx_t ctx, void* stream, int topk, const int* ids, int T, int rank,
                           int E, int* blockcount, int* blockoff, int* cta_batch, int* cta_limit,
                           int* num_non_exiting, int* total_padded, int* route_map, int* exp2perm,

@@ -37,6 +37,11 @@ class K3hArgs {
   bool ok_ = true;
 };
 
+// Workgroups of `block` threads of (module, entry) that the current device holds
+// at once (occupancy per CU x CUs), cached in the context.
+int k3h_ctx_resident(k3h_ctx_t ctx, const char* module_key, const char* entry, uint32_t block,
+                     int* out);
+
 // Look up (module, entry) in the context and launch with packed args.
 int k3h_run(k3h_ctx_t ctx, const char* module_key, const char* entry, uint32_t gx, uint32_t gy,
             uint32_t gz, uint32_t block, void* stream, const K3hArgs& a, uint32_t shmem = 0);

@@ -9,6 +9,7 @@
 #include <mutex>
 #include <new>
 #include <string>
+#include <tuple>
 #include <utility>
 
 #include "k3h.h"
@@ -87,6 +88,7 @@ K3H_API const char* k3h_error_string(int code) {
     case K3H_ENOMODULE: return "code object missing or not loadable";
     case K3H_ENOENTRY: return "entry not found in module";
     case K3H_ENOMEM: return "out of host memory";
+    case K3H_ERESIDENT: return "grid larger than the device holds at once";
     default: break;
   }
   if (code <= K3H_EHIP_BASE) return hipGetErrorString(static_cast<hipError_t>(K3H_EHIP_BASE - code));
@@ -106,7 +108,33 @@ struct k3h_ctx_s {
   std::mutex mu;
   std::map<std::string, k3h_module_t> mods;
   std::map<std::pair<std::string, std::string>, k3h_fn_t> fns;
+  // (function, block size, device) -> workgroups the device holds at once
+  std::map<std::tuple<k3h_fn_t, uint32_t, int>, int> resident;
 };
+
+int k3h_ctx_resident(k3h_ctx_t ctx, const char* module_key, const char* entry, uint32_t block,
+                     int* out) {
+  k3h_fn_t fn = nullptr;
+  int r = k3h_ctx_function(ctx, module_key, entry, &fn);
+  if (r != K3H_OK) return r;
+  int dev = 0;
+  r = k3h_hip(hipGetDevice(&dev));
+  if (r != K3H_OK) return r;
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  const auto key = std::make_tuple(fn, block, dev);
+  auto it = ctx->resident.find(key);
+  if (it == ctx->resident.end()) {
+    int per_cu = 0, cus = 0;
+    r = k3h_hip(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(
+        &per_cu, reinterpret_cast<hipFunction_t>(fn), (int)block, 0));
+    if (r != K3H_OK) return r;
+    r = k3h_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    if (r != K3H_OK) return r;
+    it = ctx->resident.emplace(key, per_cu * cus).first;
+  }
+  *out = it->second;
+  return K3H_OK;
+}
 
 extern "C" {
 

@@ -117,6 +117,12 @@ K3H_API int k3h_moe_route(k3h_ctx_t ctx, void* stream, int topk, const int* ids,
   if (T == 0)  // no ids: the tables of zero blocks (num_non_exiting = total_padded = 0)
     return k3h_moe_route_tables(ctx, stream, blockcount, 0, E, 128, blockoff, cta_batch, cta_limit,
                                 num_non_exiting, total_padded, route_map);
+  // the grid barrier needs every workgroup resident at once: refuse a device that
+  // cannot hold the grid instead of relying on the kernel's bounded wait
+  int resident = 0;
+  const int rr = k3h_ctx_resident(ctx, key.c_str(), "k3h_moe_route_fused", 512, &resident);
+  if (rr != K3H_OK) return rr;
+  if (resident < blocks) return K3H_ERESIDENT;
   K3hArgs a;
   a.ptr(ids).i32(T).i32(rank).i32(E).ptr(blockcount).ptr(blockoff).ptr(cta_batch).ptr(cta_limit);
   a.ptr(num_non_exiting).ptr(total_padded).ptr(route_map).ptr(exp2perm).ptr(sync);

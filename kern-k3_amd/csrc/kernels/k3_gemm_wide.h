@@ -130,10 +130,11 @@ struct K3wOps {
 };
 
 // Runs the workgroup's items; epi(acc, tile, cb, e) takes each item's
-// accumulators.  R = (K / 128 - 2) % 3 selects the step sequence of an item's
-// tail (the steps after the main loop's groups of three), so that every stage
-// index in the step loop is a compile-time constant; the item's stage s lives in
-// physical stage (rot + s) % 3, rot advancing by K / 128 per item.
+// accumulators.  One entry serves every K: the step loop runs KS = K / 128 steps
+// per item with the stage index S held at run time (S advances modulo 3 each
+// step), and the item's stage s lives in physical stage (rot + s) % 3, rot
+// advancing by KS per item, so the next item's first two steps load into the
+// stages the current item's last two steps free.
 template <class Epi>
 K3_DEV void k3w_run(const uint8_t* __restrict__ a, const uint8_t* __restrict__ a_sf,
                     const int* __restrict__ a_rows, const uint8_t* __restrict__ wt,

@@ -282,14 +282,22 @@ extern "C" __global__ void __launch_bounds__(32 * SCATTER_WARPS) kern_k3_moe_rou
 // 64-id chunk's per-expert counts and in-chunk ranks (bit ballots), then one
 // DPP scan per expert across the chunks, whose carry is the block's count;
 // the counts go to blockcount[b].  A grid barrier follows (the grid is at most
-// RF_MAX_BLOCKS workgroups, far below what the GPU holds at once, so every
-// workgroup is resident): thread 0 of each workgroup adds one to sync[0] and
-// waits until it reaches the grid size.  The wait is bounded: after RF_SPIN_LIMIT polls the
-// workgroup stops waiting, stores -1 to total_padded and skips phase 2 (the
-// outputs are then incomplete and total_padded says so).  Each workgroup then
-// adds one to sync[1]; the last to do so puts both words back to 0, so the
-// caller zeroes `sync` once and every later launch finds it zeroed.  Launches
-// that share one `sync` must not overlap.
+// RF_MAX_BLOCKS workgroups, and the host checks that the GPU holds all of them
+// at once before it launches): thread 0 of each workgroup adds one to sync[0]
+// and waits until it reaches the grid size.  The wait is bounded and all-or-
+// nothing: after RF_SPIN_LIMIT polls a workgroup gives up by a compare-and-swap
+// that subtracts RF_POISON from the count it last read, which succeeds only if
+// no arrival came since, so the count then stays negative and no workgroup can
+// pass afterwards; a workgroup that reads a negative count gives up too.  Every
+// arrival and the poison act on one word, so either the count reaches the grid
+// size (every workgroup passes) or it is poisoned first (none passes).  On
+// failure each workgroup writes exp2perm = -1 for its own ids (no slot is
+// local, so finalize sums nothing) and workgroup 0 writes num_non_exiting = 0
+// and total_padded = -1 (no route tile for the GEMMs or the permute); the other
+// tables are left as they were.  Each workgroup then adds one to sync[1]; the
+// last to do so puts both words back to 0, so the caller zeroes `sync` once and
+// every later launch finds it zeroed, after a failure as well.  Launches that
+// share one `sync` must not overlap.
 //
 // Phase 2 (every workgroup, from the counts of all blocks, read with agent-scope
 // loads): per expert the total and this block's prefix over the blocks before
@@ -300,6 +308,7 @@ extern "C" __global__ void __launch_bounds__(32 * SCATTER_WARPS) kern_k3_moe_rou
 // e % grid == b; workgroup 0 writes num_non_exiting and total_padded.
 #define RF_MAX_BLOCKS 256        // T <= 65536 on the one-launch path
 #define RF_SPIN_LIMIT (1 << 18)  // polls of the grid barrier before giving up
+#define RF_POISON (1 << 20)      // > RF_MAX_BLOCKS: a poisoned count never reaches the grid size
 #define RF_GROUPS 16             // block groups of the phase-2 count sums
 
 K3_DEV int rf_load(const int* p) {
@@ -375,9 +384,20 @@ extern "C" __global__ void __launch_bounds__(32 * SCATTER_WARPS) k3h_moe_route_f
   __syncthreads();
   if (threadIdx.x == 0) {
     __hip_atomic_fetch_add(&sync[0], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    int ok = 1, polls = 0;
-    while (rf_load(&sync[0]) < nblk) {
-      if (++polls > RF_SPIN_LIMIT) { ok = 0; break; }
+    int ok = 1, polls = 0, v;
+    // Bounded: past the limit each poll ends the loop (count complete, count
+    // poisoned, or this poison succeeded) unless an arrival changed the count
+    // between the load and the swap, which happens at most nblk times.
+    while ((v = rf_load(&sync[0])) < nblk) {
+      if (v < 0) { ok = 0; break; }  // another workgroup gave up
+      if (++polls > RF_SPIN_LIMIT) {
+        if (__hip_atomic_compare_exchange_strong(&sync[0], &v, v - RF_POISON, __ATOMIC_RELAXED,
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+          ok = 0;
+          break;
+        }
+        continue;
+      }
       __builtin_amdgcn_s_sleep(1);
     }
     if (__hip_atomic_fetch_add(&sync[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nblk - 1) {
@@ -387,8 +407,16 @@ extern "C" __global__ void __launch_bounds__(32 * SCATTER_WARPS) k3h_moe_route_f
     ok_s = ok;
   }
   __syncthreads();
-  if (!ok_s) {
-    if (threadIdx.x == 0) rf_store(total_padded, -1);
+  if (!ok_s) {  // no workgroup passed the barrier: publish "nothing routed"
+#pragma unroll
+    for (int r = 0; r < CPW; ++r) {
+      const int c = wave + r * nw;
+      if (c < ROUTE_CHUNKS && idx[r] < nid) exp2perm[idx[r]] = -1;
+    }
+    if (b == 0 && threadIdx.x == 0) {
+      num_non_exiting[0] = 0;
+      total_padded[0] = -1;
+    }
     return;
   }
 

@@ -28,6 +28,7 @@ BUILD = os.path.join(PKG, "build")
 LIB_PATH = os.path.join(BUILD, "libk3h.so")
 
 K3H_OK, K3H_EINVAL, K3H_ENOMODULE, K3H_ENOENTRY, K3H_ENOMEM = 0, -1, -2, -3, -4
+K3H_ERESIDENT = -5
 
 MOE_V4 = "k3_moe_prefill_v4+EP_RANKS=4+EP_STRIDED=1+TILE_SHIFT=7+SCATTER_WARPS=16"
 MOE_V3 = "k3_moe_prefill_v3+EP_STRIDED=1"

@@ -42,6 +42,7 @@ def test_error_strings():
     assert k3h.error_string(k3h.K3H_OK) == "ok"
     assert "invalid" in k3h.error_string(k3h.K3H_EINVAL)
     assert "missing" in k3h.error_string(k3h.K3H_ENOMODULE)
+    assert "at once" in k3h.error_string(k3h.K3H_ERESIDENT)
 
 
 @pytest.fixture

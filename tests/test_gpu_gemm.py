@@ -117,10 +117,11 @@ def _check_acc(got, q, sf, rows, w, wsf, cta, nt, E, N, K):
     return ref, mag, live
 
 
-# N % 512 == 0 and 256 <= K <= 3584 run the 512-column 8-wave entries
-# (kern_k3h_moe_gemm2_*_r{(K/128 - 2) % 3}: K 256 / 384 / 512 are their shortest
-# pipelines of each tail class, 3072 and 3584 the fc2 / fc1 depths); the others
-# the 256-column entries (K > 3584: the _w entries).
+# N % 512 == 0 and 256 <= K <= 3584 run the persistent 512-column 8-wave entry
+# kern_k3h_moe_gemm2_f32 (one entry for every K, its step loop runs K / 128 steps
+# with the stage index held at run time: K 256 / 384 / 512 start the next item in
+# each of the three stage rotations, 3072 and 3584 are the fc2 / fc1 depths); the
+# others the 256-column entries (K > 3584: the _w entries).
 @pytest.mark.parametrize("E,N,K,gather", [(4, 512, 1024, True), (3, 256, 3584, False),
                                           (2, 768, 256, True), (2, 256, 7168, True),
                                           (2, 512, 3584, True), (3, 1024, 3072, False),

@@ -179,6 +179,60 @@ def test_route_one_launch(ctx, T, topk):
         _eq("exp2perm", from_dev(o["e2p"]), e2p)
 
 
+def _route_expect(T, topk, seed):
+    S, bias, rs = _router_inputs(T, seed)
+    ids, _ = O.router_topk(S, bias, rs[0], T, topk)
+    nblk = (T + 255) // 256
+    cap = T * topk + E * 128
+    bc = O.route_count(ids, T, topk, RANK, E)
+    tab = O.route_tables(bc, nblk, E, 128, cap)
+    rmap, e2p = O.route_scatter(ids, tab["blockoff"], T, topk, RANK, E, tab["route_map"])
+    return ids, nblk, cap, bc, tab, rmap, e2p
+
+
+def _route_outputs(T, topk, nblk, cap):
+    def fill(n):
+        return torch.full((n,), -7, dtype=torch.int32, device="cuda")
+    return dict(bc=fill(nblk * E), bo=fill(nblk * E), cb=fill(cap // 128 + 1), cl=fill(cap // 128 + 1),
+                nne=fill(1), tp=fill(1), rmap=fill(cap), e2p=fill(T * topk))
+
+
+# The barrier's give-up path, forced from the host so that every workgroup still
+# exits normally: sync[0] preset to -1 makes the arrivals stop one short of the
+# grid size, so every workgroup's bounded wait expires and the first to give up
+# poisons the count; preset to a poisoned value, every workgroup gives up at its
+# first poll.  The outputs must say "nothing routed" (num_non_exiting 0,
+# total_padded -1, every exp2perm entry -1, the other tables untouched), `sync`
+# must come back zero, and the same `sync` must then serve a normal call.
+@pytest.mark.parametrize("T,preset", [(1, -1), (300, -1), (16384, -1), (16384, -(1 << 20))])
+def test_route_one_launch_gives_up(ctx, T, preset):
+    topk = 8
+    _case(f"one-launch routing give-up T={T} sync[0]={preset}")
+    ids, nblk, cap, bc, tab, rmap, e2p = _route_expect(T, topk, 1900 + T)
+    d_ids = to_dev(ids)
+    sync = torch.tensor([preset, 0], dtype=torch.int32, device="cuda")
+    o = _route_outputs(T, topk, nblk, cap)
+    ctx.moe_route(d_ids, T, RANK, E, o["bc"], o["bo"], o["cb"], o["cl"], o["nne"], o["tp"],
+                  o["rmap"], o["e2p"], sync, topk=topk)
+    torch.cuda.synchronize()
+    assert from_dev(sync).tolist() == [0, 0], "barrier words not reset after giving up"
+    assert from_dev(o["nne"])[0] == 0 and from_dev(o["tp"])[0] == -1
+    assert (from_dev(o["e2p"]) == -1).all(), "exp2perm not cleared on give-up"
+    _eq("blockcount", from_dev(o["bc"]), bc)  # phase 1 precedes the barrier
+    for k in ("bo", "cb", "cl", "rmap"):
+        assert (from_dev(o[k]) == -7).all(), f"{k} written although the barrier failed"
+    o = _route_outputs(T, topk, nblk, cap)
+    ctx.moe_route(d_ids, T, RANK, E, o["bc"], o["bo"], o["cb"], o["cl"], o["nne"], o["tp"],
+                  o["rmap"], o["e2p"], sync, topk=topk)
+    torch.cuda.synchronize()
+    assert from_dev(sync).tolist() == [0, 0]
+    nne, tp = tab["num_non_exiting"], tab["total_padded"]
+    assert from_dev(o["nne"])[0] == nne and from_dev(o["tp"])[0] == tp
+    _eq("blockoff", from_dev(o["bo"]), tab["blockoff"])
+    _eq("route_map", from_dev(o["rmap"])[:tp], rmap[:tp])
+    _eq("exp2perm", from_dev(o["e2p"]), e2p)
+
+
 def test_route_one_launch_empty_and_limits(ctx):
     z = torch.zeros(64, dtype=torch.int32, device="cuda")
     nne = torch.full((1,), -7, dtype=torch.int32, device="cuda")
