@@ -1,11 +1,14 @@
 // Typed wrappers: KDA span gather (K9) and output gate (K11), HEADS = 24
-// modules.  Grids are the manifest's (k3-tp4-prefill-16k.json): span_gather_v2
-// 406197 (6, 4, ceil(tokens/16)) x 128, kda_out_gate_v2 406169 (tokens, 3, 1) x 128.
+// modules.  The manifest grids (k3-tp4-prefill-16k.json) are span_gather_v2
+// 406197 (6, 4, ceil(tokens/16)) x 128 and kda_out_gate_v2 406169 (tokens, 3, 1)
+// x 128; the out gate launches the manifest's, the span gather a compact grid of
+// 256-thread workgroups that its entry also accepts.
 #include "k3h_internal.h"
 
 namespace {
 constexpr int kHeads = 24;
 constexpr int kInner = kHeads * 128;
+constexpr uint32_t kSpanShare = 2;  // 16-row tiles per span-gather workgroup
 }  // namespace
 
 extern "C" {
@@ -24,8 +27,13 @@ K3H_API int k3h_span_gather(k3h_ctx_t ctx, void* stream, const void* partial, co
   K3hArgs a;
   a.ptr(partial).ptr(cw).ptr(kda_base).ptr(line_index).i64(line_bytes).ptr(wsm_partial);
   a.ptr(span_q).ptr(span_k).ptr(span_v).ptr(span_beta).ptr(span_flow).ptr(span_at).i32(span);
-  return k3h_run(ctx, "k3_span_gather_v3+HEADS=24", "kern_k3_span_gather", kInner / 512, 4,
-                 k3h_cdiv(span, 16), 128, stream, a);
+  // Two 16-row tiles of a column per 256-thread workgroup (the second tile's
+  // taps pass through LDS): one work item per (tile pair, stream, column tile)
+  // and one beta / flow item per tile pair, as a 1-D grid.  The entry also runs
+  // the manifest's (INNER / 512, 4, ceil(span / 16)) x 128 geometry.
+  const uint32_t pairs = k3h_cdiv(k3h_cdiv(span, 16), kSpanShare);
+  return k3h_run(ctx, "k3_span_gather_v3+HEADS=24", "kern_k3_span_gather",
+                 (3 * (kInner / 512) + 1) * pairs, 1, 1, 128 * kSpanShare, stream, a);
 }
 
 K3H_API int k3h_kda_out_gate(k3h_ctx_t ctx, void* stream, const void* attn,

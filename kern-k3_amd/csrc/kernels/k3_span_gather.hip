@@ -21,18 +21,24 @@
 // blockIdx.y == 3: span_beta[h*span + i] = bf16(wsm[at+i, h]) for h < HEADS and
 // span_flow[i, 0..128) = bf16(wsm[at+i, 96..224)) (k3_span_gather_v3.cu:267-281).
 //
-// Work split: a workgroup's tile is 512 columns x 16 rows of one stream; thread
-// t owns 4 consecutive columns (one 8-byte vector per row) for all 16 rows, so
-// only 3 tap rows per 16 are read twice.  All 19 row vectors and the weights are
-// loaded (non-temporally) before any is used.  On MI355X this tile shape moves
-// the span's bytes faster than 16-byte vectors over 8-row halves (6 tap rows
-// per 16), than 16-byte vectors over 1024-column x 16-row tiles (the same
-// re-reads, half the load instructions: 113.9 against 110.9 us at 16384 rows
-// after a clean flush) and than any cacheable tap load.  Only the z == 0 workgroup
-// reads the old window, and it writes the new one after those reads.  beta /
-// flow (y == 3) are landed once per row tile.  The logistic uses the
-// hardware 2^x and reciprocal (as the reference's fast form does); the result is
-// within one bf16 ulp of the CPU checker's exact logistic.
+// Work split: a tile is 512 columns x 16 rows of one stream; thread t of a
+// tile owns 4 consecutive columns (one 8-byte vector per row) for all 16 rows,
+// and all 19 row vectors (3 taps + 16 rows) and the weights are loaded (non-
+// temporally) before any is used.  A workgroup of 128 * share threads holds
+// `share` consecutive tiles of one column strip: under the manifest's block
+// (128) one tile, under the typed call's (256) two, the second taking its three
+// taps from the first tile's last input rows through LDS, so 3 rows in 32 are
+// read twice instead of 3 in 16.  On MI355X this shape moves the span's bytes
+// faster than 16-byte vectors over 8-row halves (6 tap rows per 16), than
+// 16-byte vectors or 256-thread rows over 1024-column tiles, than four tiles
+// per workgroup, than long column strips walked with the next block's loads in
+// flight (the strips' row accesses drift apart in time and lose DRAM page
+// locality: 120-146 us against 111 us at 16384 rows) and than any cacheable tap
+// load (fast after a clean flush, 40% slower after a dirty one).  Only the
+// z == 0 tile reads the old window, and it writes the new one after those
+// reads.  beta / flow (y == 3) are landed once per row tile.  The logistic uses
+// the hardware 2^x and reciprocal (as the reference's fast form does); the
+// result is within one bf16 ulp of the CPU checker's exact logistic.
 #include "../common/k3_dev.h"
 
 #ifndef HEADS
@@ -78,31 +84,42 @@ K3_DEV k3_u2 k9_row(const float* a0, const float* a1, const float* a2, const flo
 
 K3_DEV k3_u2 k9_ld8_nt(const uint16_t* p) { return __builtin_nontemporal_load((const k3_u2*)p); }
 
-extern "C" __global__ void __launch_bounds__(128) kern_k3_span_gather(
+#define K9_SHARE_MAX 4  // 16-row tiles per workgroup (block 128 x share)
+
+extern "C" __global__ void __launch_bounds__(128 * K9_SHARE_MAX) kern_k3_span_gather(
     const uint16_t* __restrict__ partial, const float* __restrict__ cw, void* __restrict__ kda_base,
     const int* __restrict__ line_index, long long line_bytes, const float* __restrict__ wsm_partial,
     uint16_t* __restrict__ span_q, uint16_t* __restrict__ span_k, uint16_t* __restrict__ span_v,
     uint16_t* __restrict__ span_beta, uint16_t* __restrict__ span_flow,
     const int* __restrict__ span_at, int span) {
-  // Workgroups reach the XCDs round-robin by linear id.  The launch has
+  // A workgroup of 128 * share threads (share = blockDim.x / 128: 1 under the
+  // manifest's block, up to K9_SHARE_MAX) owns `share` consecutive 16-row tiles
+  // of one column tile; thread group h (threads 128 h ..) owns tile h.  Tile h's
+  // taps are tile h - 1's last three input rows, handed over through LDS, so the
+  // workgroup reads the 3 rows before its first tile only.
+  // Workgroups reach the XCDs round-robin by linear id.  The manifest launch has
   // 4 * K9_XT workgroups per row tile but only 3 * K9_XT + 1 with work, so the
-  // tiles are renumbered: linear ids [0, 3 K9_XT nz) are the stream tiles
-  // (column tile fastest, then stream, then row tile), the next nz ids the
-  // beta / flow tiles, and the rest exit.  Every XCD then gets the same share.
-  const uint32_t nz = min(gridDim.z, (uint32_t)(span + K9_ROWS - 1) / K9_ROWS);
+  // tiles are renumbered: linear ids [0, 3 K9_XT ng) are the stream tile groups
+  // (column tile fastest, then stream, then row group), the next ng ids the
+  // beta / flow groups, and the rest exit.  Every XCD then gets the same share.
+  const int share = (int)blockDim.x / 128, half = (int)threadIdx.x / 128;
+  const int tid = (int)threadIdx.x % 128;
+  const uint32_t nz = (uint32_t)(span + K9_ROWS - 1) / K9_ROWS;
+  const uint32_t ng = (nz + share - 1) / share;
   const uint32_t L = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-  uint32_t bx, by, bz;
-  if (L < 3 * K9_XT * nz) {
-    bz = L / (3 * K9_XT);
+  uint32_t bx, by, bg;
+  if (L < 3 * K9_XT * ng) {
+    bg = L / (3 * K9_XT);
     by = L % (3 * K9_XT) / K9_XT;
     bx = L % K9_XT;
-  } else if (L < (3 * K9_XT + 1) * nz) {
-    bz = L - 3 * K9_XT * nz;
+  } else if (L < (3 * K9_XT + 1) * ng) {
+    bg = L - 3 * K9_XT * ng;
     by = 3;
     bx = 0;
   } else {
     return;
   }
+  const uint32_t bz = bg * share + half;
   const int at = span_at[0];
   const int tile0 = bz * K9_ROWS;
   partial += (size_t)at * K9_KDA_FUSED;
@@ -110,7 +127,7 @@ extern "C" __global__ void __launch_bounds__(128) kern_k3_span_gather(
 
   if (by == 3) {
     // 8 threads per row: thread k lands beta for heads k, k + 8, ... and 16 flow columns
-    const int i = tile0 + (int)(threadIdx.x / 8), k = threadIdx.x % 8;
+    const int i = tile0 + tid / 8, k = tid % 8;
     if (i >= span) return;
     const float* row = wsm_partial + (size_t)i * K9_WSM;
     for (int h = k; h < HEADS; h += 8) span_beta[(size_t)h * span + i] = (uint16_t)k3_pack_bf2(row[h], 0.0f);
@@ -127,9 +144,11 @@ extern "C" __global__ void __launch_bounds__(128) kern_k3_span_gather(
   }
 
   const int s = by;
-  const int c = (int)(bx * 128 + threadIdx.x) * 4;
+  const int c = (int)(bx * 128 + tid) * 4;
   const int row0 = tile0;
-  const int nrow = min(K9_ROWS, span - row0);
+  // rows of this tile; 0 for a thread group past the span's last tile (it loads
+  // and stores nothing but still meets the workgroup barrier)
+  const int nrow = max(0, min(K9_ROWS, span - row0));
   uint16_t* __restrict__ out = s == 0 ? span_q : s == 1 ? span_k : span_v;
   const uint16_t* __restrict__ col = partial + (size_t)s * K9_INNER + c;
   const bool first = bz == 0;
@@ -146,13 +165,30 @@ extern "C" __global__ void __launch_bounds__(128) kern_k3_span_gather(
   }
   // x[j] = input row row0 - 3 + j (j < 3: taps)
   k3_u2 x[K9_ROWS + 3];
+  if (half == 0) {
 #pragma unroll
-  for (int t = 0; t < 3; ++t)
-    x[t] = first ? *(const k3_u2*)(win + (size_t)t * K9_INNER + c)
-                 : k9_ld8_nt(col + (size_t)(row0 - 3 + t) * K9_KDA_FUSED);
+    for (int t = 0; t < 3; ++t)
+      x[t] = first ? *(const k3_u2*)(win + (size_t)t * K9_INNER + c)
+                   : k9_ld8_nt(col + (size_t)(row0 - 3 + t) * K9_KDA_FUSED);
+  }
+  if (nrow > 0) {
 #pragma unroll
-  for (int r = 0; r < K9_ROWS; ++r)
-    x[3 + r] = k9_ld8_nt(col + (size_t)(row0 + min(r, nrow - 1)) * K9_KDA_FUSED);
+    for (int r = 0; r < K9_ROWS; ++r)
+      x[3 + r] = k9_ld8_nt(col + (size_t)(row0 + min(r, nrow - 1)) * K9_KDA_FUSED);
+  }
+  if (share > 1) {
+    __shared__ k3_u2 taps_s[K9_SHARE_MAX - 1][3][128];
+    if (half < share - 1 && nrow > 0) {
+#pragma unroll
+      for (int t = 0; t < 3; ++t) taps_s[half][t][tid] = x[K9_ROWS + t];
+    }
+    __syncthreads();
+    if (half > 0) {
+#pragma unroll
+      for (int t = 0; t < 3; ++t) x[t] = taps_s[half - 1][t][tid];
+    }
+  }
+  if (nrow == 0) return;
 
   // slide over the rows: each input row is unpacked once
   float a[4][4];

@@ -66,7 +66,10 @@ class Span:
         return [from_dev(o) for o in outs] + [from_dev(beta), from_dev(flow)]
 
 
-@pytest.mark.parametrize("rows,at,span", [(16384, 0, 16384), (100, 7, 45), (10, 4, 2), (40, 0, 17)])
+# spans cover the typed call's tile pairs: whole pairs (32, 16384), a pair whose
+# second tile is partial (17, 45) or past the span (65), and spans under 3 rows
+@pytest.mark.parametrize("rows,at,span", [(16384, 0, 16384), (100, 7, 45), (10, 4, 2), (40, 0, 17),
+                                          (40, 3, 32), (80, 5, 65), (8, 6, 1)])
 def test_span_gather(ctx, rows, at, span):
     _case(f"span_gather rows={rows} at={at} span={span}")
     sp = Span(rows, 2000 + span)
@@ -136,6 +139,28 @@ def test_kda_out_gate_rejects_other_eps(ctx):
         z = torch.zeros(4 * INNER, dtype=torch.bfloat16, device="cuda")
         ctx.kda_out_gate(z, z, torch.ones(128, device="cuda"), z, to_dev(np.array([0], np.int32)),
                          1, eps=1e-4)
+
+
+@pytest.mark.parametrize("span", [1000, 2048])
+def test_span_gather_manifest_geometry_matches_typed(ctx, span):
+    """The entry under the manifest's (INNER/512, 4, ceil(span/16)) x 128 grid (one
+    16-row tile per workgroup) and under the typed call's 256-thread workgroups
+    (two tiles, taps handed over in LDS) produce the same bits."""
+    ops = json.load(open(os.path.join(GOLDEN, "manifest_hot_ops.json")))
+    _case(f"span_gather manifest vs typed geometry span={span}")
+    a, b = Span(span + 2, 2400 + span), Span(span + 2, 2400 + span)
+    typed = a.run(ctx, 2, span)
+    outs = [torch.empty((span, INNER), dtype=torch.bfloat16, device="cuda") for _ in range(3)]
+    beta = torch.empty(HEADS * span, dtype=torch.bfloat16, device="cuda")
+    flow = torch.empty((span, 128), dtype=torch.bfloat16, device="cuda")
+    k3h.ManifestOp(ctx, "span_gather_v2", ops["span_gather_v2"])(
+        [b.d_partial, b.d_cw, b.d_state, b.d_line, b.d_wsm, *outs, beta, flow,
+         to_dev(np.array([2], np.int32)), span], {"tokens": span})
+    torch.cuda.synchronize()
+    man = [from_dev(o) for o in outs] + [from_dev(beta), from_dev(flow)]
+    for j in range(5):
+        assert np.array_equal(typed[j], man[j]), j
+    assert np.array_equal(a.window()[1], b.window()[1])
 
 
 def test_manifest_kda_ops(ctx):
