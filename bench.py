@@ -350,7 +350,7 @@ def bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0) -> 
     del pq, psf, x8, sf8
     fc2 = syn("5/fc2", (tpad, H))
     out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
-    add("weighted finalize (cfg 5d)", "kern_k3_moe_finalize", f"T={T} cols={H}",
+    add("weighted finalize (cfg 5d)", "k3h_moe_finalize_rows", f"T={T} cols={H}",
         live * H * 2 + 2 * T * 8 * 4 + T * H * 2,
         timed(lambda: ctx.moe_finalize(fc2, e2p, wts, out, T, H, topk=8, stream=s)),
         cpu=O and (lambda a=(h(fc2), h(e2p), h(wts)): O.moe_finalize(a[0], a[1], a[2], T, 8, H)))
@@ -667,7 +667,7 @@ OP_KERNELS = {
                                                  "kern_k3_moe_route_scatter"],
     "EP routing, one launch (k3h_moe_route)": ["k3h_moe_route_fused"],
     "MXFP8 permute (cfg 5c)": ["k3h_moe_permute_mx"],
-    "weighted finalize (cfg 5d)": ["kern_k3_moe_finalize"],
+    "weighted finalize (cfg 5d)": ["k3h_moe_finalize_rows"],
     "residual push v3 (res_in, nb 0, 4 ranks)": ["kern_k3_attnres_rms_push"],
     "residual push_add2 (res_in, nb 4, 4 ranks)": ["k3h_attnres_rms_push_nb4s"],
     "K1b nb 1 (res_mlp, typed call)": ["k3h_land_add_attnres_rms_nb1s"],

@@ -254,8 +254,10 @@ K3H_API int k3h_moe_route(k3h_ctx_t ctx, void* stream, int topk, const int* ids,
                           int* num_non_exiting, int* total_padded, int* route_map, int* exp2perm,
                           int* sync);
 /* kern_k3_moe_finalize (k3_moe_prefill_v4.cu:254; op moe_finalize, json:405686):
- * fc2 bf16 [total_padded, cols], wts f32 [T,topk] -> out bf16 [T, cols].
- * grid ceil(T/2), block 128; cols % 8 == 0. */
+ * fc2 bf16 [total_padded, cols], wts f32 [T,topk] -> out bf16 [T, cols];
+ * cols % 8 == 0.  The manifest entry runs grid ceil(T/2), block 128 (one wave per
+ * token); this call launches k3h_moe_finalize_rows of the same module, grid T,
+ * block 448 (one workgroup per token), whose outputs are the same bits. */
 K3H_API int k3h_moe_finalize(k3h_ctx_t ctx, void* stream, int topk, const void* fc2,
                              const int* exp2perm, const float* wts, void* out, int T, int cols);
 /* k3h_moe_permute_mx: no reference entry (moe_fc1 gathers through route_map

@@ -138,7 +138,9 @@ K3H_API int k3h_moe_finalize(k3h_ctx_t ctx, void* stream, int topk, const void* 
     return K3H_EINVAL;
   K3hArgs a;
   a.ptr(fc2).ptr(exp2perm).ptr(wts).ptr(out).i32(T).i32(cols);
-  return k3h_run(ctx, key.c_str(), "kern_k3_moe_finalize", k3h_cdiv(T, 2), 1, 1, 128, stream, a);
+  // one 448-thread workgroup per token (k3h_moe_finalize_rows, the same bits as
+  // the manifest entry kern_k3_moe_finalize, which gives each token one wave)
+  return k3h_run(ctx, key.c_str(), "k3h_moe_finalize_rows", (uint32_t)T, 1, 1, 448, stream, a);
 }
 
 K3H_API int k3h_moe_permute_mx(k3h_ctx_t ctx, void* stream, const void* q, const void* sf,

@@ -16,6 +16,7 @@ from k3data import from_dev, normal_bf16, rng, to_bf16, to_dev
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 E, RANK = 56, 0
+_MOE_V4 = "k3_moe_prefill_v4+EP_RANKS=4+EP_STRIDED=1+TILE_SHIFT=7+SCATTER_WARPS=16"
 
 
 def _case(m):
@@ -325,9 +326,22 @@ def test_finalize_every_slot_count(ctx, topk, cols):
     wts = g.random((T, topk), dtype=np.float32) * 2 - 0.5
     fc2 = normal_bf16(g, (rows, cols))
     out = torch.empty((T, cols), dtype=torch.bfloat16, device="cuda")
-    ctx.moe_finalize(to_dev(fc2), to_dev(e2p.reshape(-1)), to_dev(wts), out, T, cols, topk=topk)
+    d_fc2, d_e2p, d_wts = to_dev(fc2), to_dev(e2p.reshape(-1)), to_dev(wts)
+    ctx.moe_finalize(d_fc2, d_e2p, d_wts, out, T, cols, topk=topk)
     torch.cuda.synchronize()
-    _eq("finalize", from_dev(out), O.moe_finalize(fc2, e2p.reshape(-1), wts, T, topk, cols))
+    want = O.moe_finalize(fc2, e2p.reshape(-1), wts, T, topk, cols)
+    _eq("finalize", from_dev(out), want)
+    # the manifest entry (one wave per token, grid ceil(T/2) x 128), which the typed
+    # call does not launch, on the same inputs
+    key = _MOE_V4 + ("+TOPK=8" if topk == 8 else "")
+    spec = {"params": ["in buffer<bf16>", "in buffer<i32>", "in buffer<f32>", "out buffer<bf16>",
+                       "i32", "i32"],
+            "impl": {"launches": [{"module": key, "entry": "kern_k3_moe_finalize",
+                                   "grid": [{"ceil_div": ["tokens", 2]}, 1, 1], "block": [128, 1, 1]}]}}
+    out2 = torch.empty((T, cols), dtype=torch.bfloat16, device="cuda")
+    k3h.ManifestOp(ctx, "moe_finalize", spec)([d_fc2, d_e2p, d_wts, out2, T, cols], {"tokens": T})
+    torch.cuda.synchronize()
+    _eq("finalize (manifest entry)", from_dev(out2), want)
 
 
 def test_weight_layouts(ctx):
