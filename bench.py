@@ -476,6 +476,7 @@ def bench_ceilings(ctx, out_path: str | None, reps: int = 100, flushed_reps: int
                  "us_b2b": round(b2b, 2), "gbs_b2b": round(nb / b2b / 1e3, 1),
                  "us_flushed": round(fl, 2), "gbs_flushed": round(nb / fl / 1e3, 1)})
     del x, res, gm, ro, q, sf
+    rows += bench_op_shapes(ctx, launcher, time_it, reps, flushed_reps)
     # MFMA issue rate, register operands
     n_wg, iters = 256 * 2, 2000
     mout = torch.empty(n_wg * 256, dtype=torch.float32, device="cuda")
@@ -491,6 +492,85 @@ def bench_ceilings(ctx, out_path: str | None, reps: int = 100, flushed_reps: int
         with open(out_path, "w") as f:
             json.dump(rows, f, indent=1)
     return rows
+
+
+def bench_op_shapes(ctx, launcher, time_it, reps: int, flushed_reps: int) -> list:
+    """The operator-shape probes of k3h_probe next to the operators they mirror,
+    in one process on the same inputs' shapes: the KDA span gather (cfg 3a: 3-row
+    re-read per 16 or per 32 rows, or none), the weighted finalize (cfg 5d: rows
+    gathered through the config-5 routing's exp2perm, one row written per token)
+    and the MXFP8 permute's payload (cfg 5c: one row gathered per padded row).
+    Each probe's bytes are its own algorithmic bytes (re-reads not counted);
+    the operator rows carry the operators' algorithmic bytes."""
+    import torch
+    s = torch.cuda.current_stream()
+    out = []
+
+    def row(name, op, nbytes, fn, grid, note):
+        b2b, fl = time_it(fn, reps, flushed_reps)
+        r = {"probe": name, "op": op, "loads_in_flight": "-", "grid": grid, "cache": note,
+             "bytes": nbytes, "us_b2b": round(b2b, 2), "gbs_b2b": round(nbytes / b2b / 1e3, 1),
+             "us_flushed": round(fl, 2), "gbs_flushed": round(nbytes / fl / 1e3, 1)}
+        out.append(r)
+        log(f"{name:40s} {b2b:8.2f} us {r['gbs_b2b']:7.0f} GB/s back to back | "
+            f"{fl:8.2f} us {r['gbs_flushed']:7.0f} GB/s flushed")
+
+    # span gather: [T, 4 * 3072] bf16 -> 3 x [T, 3072]
+    inner = 3072
+    part = syn("3/partial", (T, 4 * inner))
+    d = [torch.empty((T, inner), dtype=torch.bfloat16, device="cuda") for _ in range(3)]
+    P5 = ["in buffer<bf16>"] + ["out buffer<bf16>"] * 3 + ["i32"]
+    span_bytes = 2 * 3 * T * inner * 2
+    for S, blk, note in ((0, 128, "no tap rows"), (1, 128, "3 tap rows per 16"), (2, 256, "3 tap rows per 32")):
+        grid = 18 * -(-T // (16 * max(S, 1)))
+        row(f"span_s{S}", "span gather shape", span_bytes,
+            launcher(f"k3h_probe_span_s{S}", grid, P5, [part, *d, T], block=blk), f"flat {grid} x {blk}",
+            f"non-temporal, {note}")
+    cw = syn("3/conv_w", (3, 4, inner), std=0.5).float()
+    state = torch.zeros(2 * 1628160, dtype=torch.uint8, device="cuda")
+    line = torch.zeros(T, dtype=torch.int32, device="cuda")
+    wsm = syn("3/wsm", (T, 256), dtype=torch.float32)
+    beta = torch.empty(24 * T, dtype=torch.bfloat16, device="cuda")
+    flow = torch.empty((T, 128), dtype=torch.bfloat16, device="cuda")
+    at0 = torch.zeros(1, dtype=torch.int32, device="cuda")
+    row("kern_k3_span_gather (the operator, cfg 3a)", "span gather", 619180032,
+        lambda: ctx.span_gather(part, cw, state, line, 1628160, wsm, *d, beta, flow, at0, T, stream=s),
+        "typed call", "non-temporal, 3 tap rows per 32")
+    del part, d, cw, state, line, wsm, beta, flow
+    # config-5 routing (the per-op table's inputs)
+    Sx = syn("5/logits", (T, 224), dtype=torch.float32)
+    bias = syn("5/bias", (224,), std=0.01, dtype=torch.float32)
+    rs = torch.full((1,), 2.5, dtype=torch.bfloat16, device="cuda")
+    idx = torch.empty((T, 8), dtype=torch.int32, device="cuda")
+    wts = torch.empty((T, 8), dtype=torch.float32, device="cuda")
+    ctx.router_topk(Sx, bias, rs, idx, wts, T, topk=8, stream=s)
+    E, nblk = 56, T // 256
+    cap = T * 8 + E * 128
+    i32 = lambda n: torch.zeros(n, dtype=torch.int32, device="cuda")
+    bc, bo, cb, cl, nne, tp = i32(nblk * E), i32(nblk * E), i32(cap // 128 + 1), i32(cap // 128 + 1), i32(1), i32(1)
+    rmap, e2p, sync = i32(cap), i32(T * 8), i32(2)
+    ctx.moe_route(idx, T, 0, E, bc, bo, cb, cl, nne, tp, rmap, e2p, sync, topk=8, stream=s)
+    torch.cuda.synchronize()
+    tpad, live = int(tp.item()), int((e2p >= 0).sum().item())
+    fc2 = syn("5/fc2", (tpad, H))
+    fo = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    fin_bytes = live * H * 2 + 2 * T * 8 * 4 + T * H * 2
+    row("gather", "finalize shape", live * H * 2 + T * 8 * 4 + T * H * 2,
+        launcher("k3h_probe_gather", T, ["in buffer<bf16>", "in buffer<i32>", "out buffer<bf16>", "i32", "i32"],
+                 [fc2, e2p, fo, T, H], block=448), f"flat {T} x 448", "non-temporal, rows through exp2perm")
+    row("k3h_moe_finalize_rows (the operator, cfg 5d)", "finalize", fin_bytes,
+        lambda: ctx.moe_finalize(fc2, e2p, wts, fo, T, H, topk=8, stream=s), "typed call", "non-temporal")
+    del fc2, fo
+    x8 = torch.ones((T, H), dtype=torch.uint8, device="cuda")
+    sf8 = torch.ones((T, H // 32), dtype=torch.uint8, device="cuda")
+    pq = torch.empty((tpad, H), dtype=torch.uint8, device="cuda")
+    psf = torch.empty((tpad, H // 32), dtype=torch.uint8, device="cuda")
+    row("rowgather", "permute shape (payload)", 2 * tpad * H,
+        launcher("k3h_probe_rowgather", -(-tpad // 4), ["in buffer<u8>", "in buffer<i32>", "out buffer<u8>", "i32", "i32"],
+                 [x8, rmap, pq, tpad, H]), f"flat {-(-tpad // 4)} x 256", "non-temporal, one row per wave")
+    row("k3h_moe_permute_mx (the operator, cfg 5c)", "permute", 2 * tpad * (H + H // 32),
+        lambda: ctx.moe_permute_mx(x8, sf8, rmap, tp, H, pq, psf, stream=s), "typed call", "non-temporal")
+    return out
 
 
 def ceilings_markdown(rows: list) -> str:

@@ -19,6 +19,24 @@
 //   suffix _c: cacheable loads and stores instead of non-temporal ones.
 //   The host keeps n16 a multiple of 256 U (no bounds checks in the loops).
 //
+// Operator-shape probes (the byte patterns of three operators, with their
+// arithmetic replaced by moves or xors):
+//   k3h_probe_span_s<S>(src, d0, d1, d2, rows)   the KDA span gather: src
+//       [rows, 4 * 3072] bf16 (bands 0-2 read), d_s [rows, 3072]; a workgroup of
+//       128 S threads holds S tiles of 16 rows x 512 columns of one band, each
+//       thread one 8-byte vector per row; the first tile of a workgroup also
+//       loads the 3 rows before it (the conv taps), so S = 1 reads 3 rows in 16
+//       twice and S = 2 (the typed call's shape) 3 in 32; S = 0: 16-row tiles of
+//       128 threads without the tap rows (no re-read).  Grid 18 ceil(rows / 16
+//       max(S, 1)).  Every input row vector is stored unchanged.
+//   k3h_probe_gather(src, idx, dst, T, cols)   the weighted finalize: token t
+//       = workgroup t (448 threads) gathers the rows src[idx[t, k]] with
+//       idx >= 0 (k < 8) and writes their xor (zero if none) to dst[t]; each
+//       thread 2 vectors of 16 bytes per row, every row load before any store.
+//   k3h_probe_rowgather(src, idx, dst, R, cols)   the MXFP8 permute's payload:
+//       dst[r] = src[idx[r]] (cols bytes, cols % 1024 == 0), one wave per row,
+//       4 rows per 256-thread workgroup, all of a row's loads before its stores.
+//
 // MFMA probe: k3h_probe_mfma_<A><B>(out, iters), block 256, any grid: each
 // wave issues iters x 4 independent v_mfma_scale_f32_32x32x64_f8f6f4 on
 // register operands (A format e4m3 "f8" or e2m1 "f4", likewise B; unit scales);
@@ -131,6 +149,110 @@ KP_ENTRIES(u8, 8, false, true)
 KP_ENTRIES(u4p, 4, true, true)
 KP_ENTRIES(u8p, 8, true, true)
 KP_ENTRIES(u4_c, 4, false, false)
+
+// ---------------------------------------------------------------- operator shapes
+template <int S>
+K3_DEV void kp_span(const uint16_t* __restrict__ src, uint16_t* __restrict__ d0,
+                    uint16_t* __restrict__ d1, uint16_t* __restrict__ d2, int rows) {
+  constexpr int INNER = 3072, FUSED = 4 * INNER, XT = INNER / 512, SH = S > 0 ? S : 1;
+  const int g = blockIdx.x / (3 * XT), sx = blockIdx.x % (3 * XT), st = sx / XT, x = sx % XT;
+  const int half = threadIdx.x / 128, tid = threadIdx.x % 128;
+  const int row0 = (g * SH + half) * 16;
+  if (row0 >= rows) return;
+  const int c = (x * 128 + tid) * 4;
+  const uint16_t* col = src + (size_t)st * INNER + c;
+  uint16_t* out = (st == 0 ? d0 : st == 1 ? d1 : d2) + c;
+  k3_u2 v[19];
+  const bool taps = S > 0 && half == 0;
+#pragma unroll
+  for (int t = 0; t < 3; ++t)
+    if (taps) v[t] = __builtin_nontemporal_load((const k3_u2*)(col + (size_t)max(row0 - 3 + t, 0) * FUSED));
+#pragma unroll
+  for (int r = 0; r < 16; ++r)
+    v[3 + r] = __builtin_nontemporal_load((const k3_u2*)(col + (size_t)min(row0 + r, rows - 1) * FUSED));
+  k3_u2 tx = {0u, 0u};
+  if (taps) tx = v[0] ^ v[1] ^ v[2];
+#pragma unroll
+  for (int r = 0; r < 16; ++r)
+    if (row0 + r < rows) __builtin_nontemporal_store(v[3 + r] ^ (r == 0 ? tx : (k3_u2){0u, 0u}),
+                                                     (k3_u2*)(out + (size_t)(row0 + r) * INNER));
+}
+extern "C" __global__ void __launch_bounds__(128) k3h_probe_span_s0(
+    const uint16_t* src, uint16_t* d0, uint16_t* d1, uint16_t* d2, int rows) {
+  kp_span<0>(src, d0, d1, d2, rows);
+}
+extern "C" __global__ void __launch_bounds__(128) k3h_probe_span_s1(
+    const uint16_t* src, uint16_t* d0, uint16_t* d1, uint16_t* d2, int rows) {
+  kp_span<1>(src, d0, d1, d2, rows);
+}
+extern "C" __global__ void __launch_bounds__(256) k3h_probe_span_s2(
+    const uint16_t* src, uint16_t* d0, uint16_t* d1, uint16_t* d2, int rows) {
+  kp_span<2>(src, d0, d1, d2, rows);
+}
+
+template <int NS>
+K3_DEV void kp_gather_rows(const k3_u4* __restrict__ src, const int* srow, k3_u4* __restrict__ drow,
+                           int nvec, int tid) {
+  k3_u4 x[NS][2];
+#pragma unroll
+  for (int i = 0; i < NS; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      x[i][j] = __builtin_nontemporal_load(src + (size_t)srow[i] * nvec + min(tid + 448 * j, nvec - 1));
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    k3_u4 o = x[0][j];
+#pragma unroll
+    for (int i = 1; i < NS; ++i) o ^= x[i][j];
+    __builtin_nontemporal_store(o, drow + min(tid + 448 * j, nvec - 1));
+  }
+}
+extern "C" __global__ void __launch_bounds__(448) k3h_probe_gather(
+    const k3_u4* __restrict__ src, const int* __restrict__ idx, k3_u4* __restrict__ dst, int T,
+    int cols) {
+  const int t = blockIdx.x, lane = threadIdx.x & 63, nvec = cols / 8;
+  if (t >= T) return;
+  const int p = lane < 8 ? idx[(size_t)t * 8 + lane] : -1;
+  uint64_t m = __ballot(p >= 0);
+  const int n = __builtin_popcountll(m);
+  int srow[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    srow[i] = __builtin_amdgcn_readfirstlane(__shfl(p, m ? __builtin_ctzll(m) : 0, 64));
+    m &= m - 1;
+  }
+  k3_u4* drow = dst + (size_t)t * nvec;
+  switch (n) {
+    case 0:
+      for (int v = threadIdx.x; v < nvec; v += 448) __builtin_nontemporal_store((k3_u4){0u, 0u, 0u, 0u}, drow + v);
+      break;
+    case 1: kp_gather_rows<1>(src, srow, drow, nvec, threadIdx.x); break;
+    case 2: kp_gather_rows<2>(src, srow, drow, nvec, threadIdx.x); break;
+    case 3: kp_gather_rows<3>(src, srow, drow, nvec, threadIdx.x); break;
+    case 4: kp_gather_rows<4>(src, srow, drow, nvec, threadIdx.x); break;
+    case 5: kp_gather_rows<5>(src, srow, drow, nvec, threadIdx.x); break;
+    case 6: kp_gather_rows<6>(src, srow, drow, nvec, threadIdx.x); break;
+    case 7: kp_gather_rows<7>(src, srow, drow, nvec, threadIdx.x); break;
+    default: kp_gather_rows<8>(src, srow, drow, nvec, threadIdx.x); break;
+  }
+}
+
+extern "C" __global__ void __launch_bounds__(256) k3h_probe_rowgather(
+    const k3_u4* __restrict__ src, const int* __restrict__ idx, k3_u4* __restrict__ dst, int R,
+    int cols) {
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63, nvec = cols / 16;
+  if (r >= R) return;
+  const k3_u4* s = src + (size_t)idx[r] * nvec;
+  k3_u4* d = dst + (size_t)r * nvec;
+  for (int v0 = 0; v0 < nvec; v0 += 64 * 8) {
+    k3_u4 x[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = __builtin_nontemporal_load(s + min(v0 + lane + 64 * j, nvec - 1));
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (v0 + lane + 64 * j < nvec) __builtin_nontemporal_store(x[j], d + v0 + lane + 64 * j);
+  }
+}
 
 // ---------------------------------------------------------------- MFMA rate
 template <int FA, int FB>
