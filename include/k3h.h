@@ -342,7 +342,11 @@ K3H_API int k3h_mla_rope_pack(k3h_ctx_t ctx, void* stream, const void* latent,
  *   K3H_GEMM_SITU_MX  gated weights: x = bf16(situ(bf16(gate), bf16(up);
  *                     alpha[e], beta[e])) -> out e4m3 [.., N/2] (16-byte
  *                     aligned), out_sf E8M0 [.., N/64] (2-byte aligned),
- *                     quantised as kern_k3_moe_quant (fc1).
+ *                     quantised as kern_k3_moe_quant (fc1);
+ *   K3H_GEMM_F32_SITU_TILING  out f32 [tiles*128, N] (16-byte aligned) from the
+ *                     K3H_GEMM_SITU_MX kernel's own tiling, item split and
+ *                     operand roles (the same values as K3H_GEMM_F32): checks
+ *                     of the fc1 kernel's accumulators; not a serving path.
  * Work items are (tile < min(*num_tiles, max_tiles), 256-column block); the
  * workgroups hand them out per XCD (each XCD a contiguous share of the tiles and
  * columns, so that its L2 holds the operands its workgroups share); the grid
@@ -355,6 +359,7 @@ K3H_API int k3h_mla_rope_pack(k3h_ctx_t ctx, void* stream, const void* latent,
 #define K3H_GEMM_F32 0
 #define K3H_GEMM_BF16 1
 #define K3H_GEMM_SITU_MX 2
+#define K3H_GEMM_F32_SITU_TILING 3
 K3H_API int k3h_moe_w_tile(k3h_ctx_t ctx, void* stream, const void* src, void* dst, int experts,
                            int n, int k, int gated);
 K3H_API int k3h_moe_sf_tile(k3h_ctx_t ctx, void* stream, const void* src, void* dst, int experts,

@@ -128,6 +128,11 @@ K3H_API int k3h_moe_gemm_mx(k3h_ctx_t ctx, void* stream, int epilogue, const voi
       args.ptr(out);
       entry = wide ? "kern_k3h_moe_gemm_bf16_w" : "kern_k3h_moe_gemm_bf16";
       break;
+    case K3H_GEMM_F32_SITU_TILING:
+      if (!k3h_okp(out, 16)) return K3H_EINVAL;
+      args.ptr(out);
+      entry = wide ? "kern_k3h_moe_gemm_situ_acc_w" : "kern_k3h_moe_gemm_situ_acc";
+      break;
     case K3H_GEMM_SITU_MX:
       if (!k3h_okp(out, 16) || !k3h_okp(out_sf, 2) || !k3h_okp(alpha, 4) || !k3h_okp(beta, 4))
         return K3H_EINVAL;
@@ -140,9 +145,9 @@ K3H_API int k3h_moe_gemm_mx(k3h_ctx_t ctx, void* stream, int epilogue, const voi
   if (max_tiles == 0) return K3H_OK;
   // f32 / bf16 epilogues on 512-column items: persistent 8-wave workgroups
   // (kern_k3h_moe_gemm2_*, one per CU, grid a multiple of the 8 XCDs) where the
-  // shape allows them; else, and for the SiTU-GLU + MXFP8 epilogue, 256-column
+  // shape allows them; else, and for the SiTU-GLU + MXFP8 epilogue and its f32 tiling, 256-column
   // items on 4-wave workgroups (two per CU).
-  if (epilogue != K3H_GEMM_SITU_MX && N % kTileNWide == 0 && K >= 2 * kStepK &&
+  if ((epilogue == K3H_GEMM_F32 || epilogue == K3H_GEMM_BF16) && N % kTileNWide == 0 && K >= 2 * kStepK &&
       K <= kMaxKNarrow && k3h_aligned(out, 16)) {
     int cus = 0;
     if (const int rc = stream_cus(stream, &cus)) return rc;

@@ -665,6 +665,33 @@ K3_DEV void k3g_gemm_situ_mx(K3G_PARAMS, uint8_t* __restrict__ out_q, uint8_t* _
   });
 }
 
+// The fc1 entry's tiling with its accumulators stored as f32 instead of the
+// SiTU-GLU + MXFP8 epilogue: the same items, item split and swapped operand roles
+// as kern_k3h_moe_gemm_situ_mx, so a check of these accumulators (against the
+// other f32 entries, bit for bit, and as the input of the CPU epilogue) checks
+// the shipped fc1 kernel's products on every row.  Lane (j, h) of tile (mt, nt)
+// holds row 32 (2 wm + mt) + j and columns 32 (4 wn + nt) + 8 g + 4 h + 0..3 in
+// accumulators 4 g .. 4 g + 3.
+template <int KGM>
+K3_DEV void k3g_gemm_situ_acc(K3G_PARAMS, float* __restrict__ out) {
+  k3g_items<KGM, true>(a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch, E, N, K, max_tiles,
+                       [&](k3_v16f(&acc)[2][4], int tile, int cb, int, int lane, int wm, int wn) {
+    const int h = lane >> 5, j = lane & 31;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      float* orow = out + ((size_t)tile * K3G_TILE_M + 32 * (2 * wm + mt) + j) * N;
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        float* o = orow + cb * K3G_TILE_N + 32 * (4 * wn + nt) + 4 * h;
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *(k3_u4*)(o + 8 * g) = (k3_u4){__float_as_uint(acc[mt][nt][4 * g]), __float_as_uint(acc[mt][nt][4 * g + 1]),
+                                         __float_as_uint(acc[mt][nt][4 * g + 2]), __float_as_uint(acc[mt][nt][4 * g + 3])};
+      }
+    }
+  });
+}
+
 // Entries: K <= 3584 (A-scale table of 112 bytes per row, two workgroups per CU)
 // and, suffix _w, K <= 7168 (224 bytes per row, one workgroup per CU).
 #define K3G_ARGS a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch, E, N, K, max_tiles
@@ -683,6 +710,10 @@ K3_DEV void k3g_gemm_situ_mx(K3G_PARAMS, uint8_t* __restrict__ out_q, uint8_t* _
                                      const float* __restrict__ alpha,                            \
                                      const float* __restrict__ beta) {                           \
     k3g_gemm_situ_mx<KGM>(K3G_ARGS, out_q, out_sf, alpha, beta);                                 \
+  }                                                                                              \
+  extern "C" __global__ void __launch_bounds__(256, K3G_WAVES_PER_EU)                            \
+      kern_k3h_moe_gemm_situ_acc##SUF(K3G_PARAMS, float* __restrict__ out) {                     \
+    k3g_gemm_situ_acc<KGM>(K3G_ARGS, out);                                                       \
   }
 K3G_ENTRIES(, 112)
 K3G_ENTRIES(_w, 224)

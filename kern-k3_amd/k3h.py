@@ -655,7 +655,7 @@ class Ctx:
                                         _ptr(q_out), theta, eps, T, H), "mla_rope_pack")
 
     # ------------------------------------------------------------ MoE expert GEMMs
-    GEMM_F32, GEMM_BF16, GEMM_SITU_MX = 0, 1, 2
+    GEMM_F32, GEMM_BF16, GEMM_SITU_MX, GEMM_F32_SITU_TILING = 0, 1, 2, 3
 
     def moe_w_tile(self, src, dst, experts: int, n: int, k: int, gated: int, stream=None) -> None:
         """Row-major e2m1 weights [experts, n, k/2] -> the MFMA-operand tiled layout."""
@@ -676,7 +676,8 @@ class Ctx:
     def moe_gemm_mx(self, epilogue: int, a, a_sf, a_rows, wt, wsf, num_tiles, cta_batch,
                     max_tiles: int, E: int, N: int, K: int, out, out_sf=None, alpha=None,
                     beta=None, stream=None) -> None:
-        """MX GEMM over the route tiles (epilogue GEMM_F32 / GEMM_BF16 / GEMM_SITU_MX)."""
+        """MX GEMM over the route tiles (epilogue GEMM_F32 / GEMM_BF16 / GEMM_SITU_MX, or
+        GEMM_F32_SITU_TILING: the f32 accumulators of the GEMM_SITU_MX kernel's own tiling)."""
         rows = max_tiles * 128
         if a_rows is None:
             # A is read in place: one row per padded row of every tile (32-bit row offsets)
@@ -694,6 +695,8 @@ class Ctx:
         _dev(cta_batch, "cta_batch", I32, max_tiles, align=4)
         if epilogue == self.GEMM_F32:
             _dev(out, "out", F32, rows * N, align=4)
+        elif epilogue == self.GEMM_F32_SITU_TILING:
+            _dev(out, "out", F32, rows * N, align=16)
         elif epilogue == self.GEMM_BF16:
             _dev(out, "out", BF16, rows * N, align=16)
         else:

@@ -411,8 +411,13 @@ def moe_fc1_epilogue(c, alpha_rows, beta_rows):
     up16, gate16 = bf(np.ascontiguousarray(c[:, :half])), bf(np.ascontiguousarray(c[:, half:]))
     u = (up16.astype(np.uint32) << 16).view(np.float32)
     g = (gate16.astype(np.uint32) << 16).view(np.float32)
-    x = np.empty((rows, half), np.float32)
-    for r in range(rows):
-        x[r] = situ_ab(g[r], u[r], float(alpha_rows[r]), float(beta_rows[r]))
+    alpha_rows = np.asarray(alpha_rows, np.float32)
+    beta_rows = np.asarray(beta_rows, np.float32)
+    if rows and (alpha_rows == alpha_rows[0]).all() and (beta_rows == beta_rows[0]).all():
+        x = situ_ab(g, u, float(alpha_rows[0]), float(beta_rows[0]))  # one call for every row
+    else:
+        x = np.empty((rows, half), np.float32)
+        for r in range(rows):
+            x[r] = situ_ab(g[r], u[r], float(alpha_rows[r]), float(beta_rows[r]))
     x16 = bf(x)
     return moe_quant(x16, rows, half)

@@ -237,11 +237,12 @@ def _grid_rows(max_tiles, nc):
     return -(-need // nc)
 
 
-@pytest.mark.parametrize("K", [256, 384, 1536])
+@pytest.mark.parametrize("K", [256, 384, 1536, 3072, 3584])
 def test_wide_items_match_4wave(ctx, K):
     """The persistent 512-column entries (kern_k3h_moe_gemm2_f32 / _bf16, which the
     typed calls take for N % 512 == 0 and K <= 3584) against the 4-wave entries
-    launched directly, bit for bit, at a size where every workgroup runs several
+    launched directly and against the fc1 kernel's tiling (GEMM_F32_SITU_TILING),
+    bit for bit, at K up to fc1's 3584, at a size where every workgroup runs several
     items back to back (the step pipeline crossing items) and some tiles have an
     out-of-range expert or lie past the live count.  The 4-wave entries are pinned
     against the oracle by the tests above."""
@@ -276,7 +277,15 @@ def test_wide_items_match_4wave(ctx, K):
         k3h._check(ctx.L.k3h_launch(fn, grid, block, 0, None, ctypes.cast(cbuf, ctypes.c_void_p),
                                     len(args)), entry)
         torch.cuda.synchronize()
-        a, b = from_dev(got), from_dev(ref)
-        same = (a.view(np.uint8) == b.view(np.uint8)).all()
+        same = torch.equal(got.view(torch.uint8), ref.view(torch.uint8))
         print(f"  {entry}: identical = {same}", flush=True)
         assert same
+        if ep == ctx.GEMM_F32:
+            # the fc1 kernel's tiling (256-column items, swapped operand roles)
+            fc1t = torch.full_like(got, fill)
+            ctx.moe_gemm_mx(ctx.GEMM_F32_SITU_TILING, dq, dsf, dr, wt, st, nt, dcta, max_tiles, E, N,
+                            K, fc1t)
+            torch.cuda.synchronize()
+            same = torch.equal(got.view(torch.uint8), fc1t.view(torch.uint8))
+            print(f"  kern_k3h_moe_gemm_situ_acc: identical = {same}", flush=True)
+            assert same
