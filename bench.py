@@ -69,8 +69,28 @@ def make_inputs(rows: int):
             syn("2/gamma", (H,), 1.0, 0.1))
 
 
-def cpu_baseline(x, res, gamma, gpu_out, budget_s: float = 10.0) -> dict:
-    """Times the C oracle (the checker) on the same inputs, bounded to ~budget_s."""
+def native_oracle() -> str:
+    """Builds the C oracle with -march=native for the host this runs on, into a
+    directory of its own, and points oracle.py at it (K3_ORACLE_LIB) for the CPU
+    baseline; the in-tree portable build (x86-64-v3) stays the tests' checker.
+    Returns a note for the JSON line."""
+    import subprocess
+    import tempfile
+    path = os.path.join(tempfile.mkdtemp(prefix="k3oracle_"), "libk3oracle_native.so")
+    r = subprocess.run(["make", "-s", "-C", os.path.join(REPO, "oracle"), "ARCH=native", f"LIB={path}"],
+                       stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if r.returncode == 0 and os.path.exists(path):
+        os.environ["K3_ORACLE_LIB"] = path
+        return "gcc -O3 -march=native -fopenmp build of oracle/ on this host"
+    log(f"native oracle build failed, timing the portable build: {r.stdout[-300:]}")
+    return "portable (x86-64-v3) build of oracle/ (the native build failed on this host)"
+
+
+def cpu_baseline(x, res, gamma, gpu_out, budget_s: float = 10.0, build_note: str = "") -> dict:
+    """Times the C oracle (the checker) on the same inputs: inputs copied into
+    buffers that the OpenMP threads touch first, outputs allocated once outside
+    the timed calls (first touched by the threads in the warm-up call), one
+    warm-up, then the median of 5 calls (fewer if they exceed ~budget_s)."""
     import numpy as np
     import torch
     sys.path.insert(0, os.path.join(REPO, "oracle"))
@@ -79,26 +99,30 @@ def cpu_baseline(x, res, gamma, gpu_out, budget_s: float = 10.0) -> dict:
     def h(t):
         return t.cpu().view(torch.int16).numpy().view(np.uint16)
 
-    xh, rh, gh = h(x), h(res), h(gamma)
+    xh, rh, gh = O.par_copy(h(x)), O.par_copy(h(res)), O.par_copy(h(gamma))
     rows = xh.shape[0]
+    outs = (np.empty((rows, H), np.uint16), np.empty((rows, H), np.uint8),
+            np.empty((rows, H // 32), np.uint8), None)
+    O.residual_rms_mxfp8(xh, rh, gh, rows, 1e-6, want_normed=False, out=outs)  # warm-up
     times = []
     t_start = time.perf_counter()
-    out = None
-    while not times or (time.perf_counter() - t_start < budget_s and len(times) < 5):
+    while len(times) < 5 and (not times or time.perf_counter() - t_start < budget_s):
         t0 = time.perf_counter()
-        out = O.residual_rms_mxfp8(xh, rh, gh, rows, 1e-6, want_normed=False)
+        O.residual_rms_mxfp8(xh, rh, gh, rows, 1e-6, want_normed=False, out=outs)
         times.append(time.perf_counter() - t0)
-    best = sorted(times)[len(times) // 2]
+    med = sorted(times)[len(times) // 2]
     ro, q, sf = (t.cpu().numpy() if t.dtype != torch.bfloat16 else h(t) for t in gpu_out)
-    match = bool((out[0] == ro).all() and (out[1] == q).all() and (out[2] == sf).all())
+    match = bool((outs[0] == ro).all() and (outs[1] == q).all() and (outs[2] == sf).all())
     return {
-        "value": round(algo_bytes(rows) / best / 1e9, 2),
+        "value": round(algo_bytes(rows) / med / 1e9, 2),
         "unit": "GB/s",
         "cores": O.num_threads(),
         "kind": "port",
-        "sample": f"full {rows}x{H} workload, median of {len(times)} oracle passes "
-                  f"({best * 1e3:.0f} ms each) on {O.num_threads()} OpenMP threads of "
-                  f"{os.cpu_count()} hardware threads; bit-exact vs GPU: {match}",
+        "sample": f"full {rows}x{H} workload: 1 warm-up, median of {len(times)} timed oracle passes "
+                  f"({med * 1e3:.0f} ms each), inputs first touched by the threads, outputs "
+                  f"allocated outside the timed calls; {O.num_threads()} OpenMP threads "
+                  f"(omp_get_max_threads) of {os.cpu_count()} hardware threads; {build_note}; "
+                  f"bit-exact vs GPU: {match}",
     }
 
 
@@ -126,13 +150,14 @@ def copy_ceiling(ctx, rows: int, reps: int) -> float:
 
 def cpu_timer(budget_s: float):
     """Times one oracle call (the checker, run as a reported baseline): one untimed
-    call, then up to 3 timed calls within `budget_s`; returns the median in s."""
+    warm-up call, then up to 5 timed calls within `budget_s`; returns the median
+    in s.  These per-op calls allocate their outputs inside the call."""
     def run(fn):
         t0 = time.perf_counter()
         fn()
         first = time.perf_counter() - t0
         times = []
-        while len(times) < 3 and (not times or sum(times) + first < budget_s):
+        while len(times) < 5 and (not times or sum(times) + first < budget_s):
             t0 = time.perf_counter()
             fn()
             times.append(time.perf_counter() - t0)
@@ -140,7 +165,16 @@ def cpu_timer(budget_s: float):
     return run
 
 
-def bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0) -> list:
+def bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0, graph: bool = False) -> list:
+    """Runs _bench_ops on a stream of its own (a HIP graph is captured from a
+    non-default stream); see _bench_ops."""
+    import torch
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        return _bench_ops(ctx, reps, out_path, cpu_budget, graph)
+
+
+def _bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0, graph: bool = False) -> list:
     """Every op at its BASELINE config shape: 5 warm-up launches, then `reps`
     launches each between two HIP events on the launch stream, with the caches
     flushed before each launch (outside the events); median, p10, p90.  Two
@@ -149,6 +183,10 @@ def bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0) -> 
     write-back), "dirty" writes a 512 MB buffer (the op then also pays for
     writing back the dirty lines its own traffic evicts).  The clean figures
     are the table's; the dirty ones are reported beside them.
+    With graph, each op's time inside a HIP graph is measured too (graph_time
+    below: rounds of a clean 512 MB read and the op, against the reads alone):
+    the reference times its prefill as graph replays, and for the short ops
+    (config 1, rms) the eager per-launch figure carries the launch.
     With cpu_budget > 0, the rows of BASELINE configs 1-5 also time the C oracle
     (OpenMP over the host cores) on host copies of the same inputs."""
     import numpy as np
@@ -165,9 +203,12 @@ def bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0) -> 
         if t.dtype == torch.bfloat16:
             return np.ascontiguousarray(t.cpu().view(torch.int16).numpy().view(np.uint16))
         return np.ascontiguousarray(t.cpu().numpy())
+    import ctypes
+    import k3h
     s = torch.cuda.current_stream()
     flush = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
     flush_rd = torch.ones(128 << 20, dtype=torch.float32, device="cuda")
+    rd_sink = torch.zeros(256, dtype=torch.int32, device="cuda")
     g = torch.Generator(device="cuda")
     g.manual_seed(24301)
 
@@ -194,7 +235,52 @@ def bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0) -> 
             ts.sort()
             pick = lambda f: ts[min(len(ts) - 1, int(f * len(ts)))]
             out += [pick(0.5), pick(0.1), pick(0.9)]
+        if graph:
+            out.append(graph_time(fn))
         return tuple(out)
+
+    # in-graph time of one op: a graph of GR rounds of (clean 512 MB read, op) against
+    # a graph of GR clean reads alone, each replayed `reps` times; the difference of
+    # the median replay times over GR is the op's incremental time inside a graph
+    # (its kernels' dispatch inside the graph included, the graph launch excluded)
+    GR = 20
+    rd_fn = ctx.function("k3h_probe", "k3h_probe_read_u4")
+    rd_n16 = flush_rd.numel() * 4 // 16
+    rd_buf = k3h.pack_args(["in buffer<u8>", "i64", "out buffer<u32>"], [flush_rd, rd_n16, rd_sink])
+    rd_c = ctypes.create_string_buffer(rd_buf, len(rd_buf))
+    rd_g, rd_b = (ctypes.c_uint32 * 3)(rd_n16 // 1024, 1, 1), (ctypes.c_uint32 * 3)(256, 1, 1)
+
+    def clean_read():
+        rc = ctx.L.k3h_launch(rd_fn, rd_g, rd_b, 0, s.cuda_stream, ctypes.cast(rd_c, ctypes.c_void_p), len(rd_buf))
+        if rc:
+            raise k3h.K3HError(rc, "k3h_probe_read_u4")
+
+    def replay_med(body):
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr, stream=s):
+            for _ in range(GR):
+                body()
+        for _ in range(2):
+            gr.replay()
+        ts = []
+        for _ in range(max(5, reps // 2)):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            gr.replay()
+            e1.record(s)
+            e1.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e3)
+        del gr
+        return sorted(ts)[len(ts) // 2]
+
+    def graph_time(fn):
+        try:
+            with_op = replay_med(lambda: (clean_read(), fn()))
+            base = replay_med(clean_read)
+        except Exception as exc:  # an op whose launches cannot be captured
+            log(f"graph capture failed: {exc}")
+            return None
+        return (with_op - base) / GR
 
     rows = []
 
@@ -207,6 +293,8 @@ def bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0) -> 
                "gbs": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1),
                "us_dirty": round(us_d, 2), "gbs_dirty": round(nbytes / (us_d * 1e-6) / 1e9, 1),
                "note": note}
+        if len(t) > 6 and t[6] is not None:
+            row.update({"us_graph": round(t[6], 2), "gbs_graph": round(nbytes / (t[6] * 1e-6) / 1e9, 1)})
         cpu_txt = ""
         if cpu is not None and O is not None:
             sec = cpu_run(cpu)
@@ -214,8 +302,9 @@ def bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0) -> 
                         "cpu_threads": O.num_threads()})
             cpu_txt = f" | CPU {sec * 1e3:8.1f} ms {nbytes / sec / 1e9:6.2f} GB/s"
         rows.append(row)
+        gtxt = f" | graph {row['us_graph']:8.2f} us" if "us_graph" in row else ""
         log(f"{op:42s} {us:8.2f} us (p10 {p10:7.2f}, p90 {p90:7.2f}) {gbs:7.0f} GB/s "
-            f"{100 * gbs / PEAK_GBS:5.1f}% | dirty {us_d:8.2f} us{cpu_txt}  {note}")
+            f"{100 * gbs / PEAK_GBS:5.1f}% | dirty {us_d:8.2f} us{gtxt}{cpu_txt}  {note}")
 
     T = 16384
     # copy ceiling
@@ -891,10 +980,12 @@ def ops_markdown(ops_json: str) -> str:
     ops = json.load(open(ops_json))
     copy = next((r["gbs"] for r in ops if r["kernel"] == "k3h_stream_copy"), None)
     thr = next((r["cpu_threads"] for r in ops if "cpu_threads" in r), None)
+    gr = any("us_graph" in r for r in ops)
+    gh, gs = ("| us, graph replay | GB/s, graph replay ", "---:|---:|") if gr else ("", "")
     out = ["| op | kernel | shape | algorithmic bytes | median us | p10 us | p90 us | GB/s | % of 8 TB/s "
-           "| % of copy | us, dirty flush | GB/s, dirty flush "
+           f"| % of copy | us, dirty flush | GB/s, dirty flush {gh}"
            f"| CPU ms{f' ({thr} threads)' if thr else ''} | CPU GB/s | GPU / CPU | note |",
-           "|---|---|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---|"]
+           f"|---|---|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|{gs}---:|---:|---:|---|"]
     for r in ops:
         if r.get("bound") == "mfma":
             continue
@@ -902,6 +993,8 @@ def ops_markdown(ops_json: str) -> str:
              if "cpu_ms" in r else " | | ")
         pc = f"{100 * r['gbs'] / copy:.0f}" if copy else ""
         d = f"{r['us_dirty']:.2f} | {r['gbs_dirty']:.1f}" if "us_dirty" in r else " | "
+        if gr:
+            d += (f" | {r['us_graph']:.2f} | {r['gbs_graph']:.1f}" if "us_graph" in r else " | | ")
         out.append(f"| {r['op']} | `{r['kernel']}` | {r['shape']} | {r['bytes']:,} | {r['us']:.2f} | "
                    f"{r['us_p10']:.2f} | {r['us_p90']:.2f} | {r['gbs']:.1f} | {r['pct_peak']:.1f} | {pc} | "
                    f"{d} | {c} | {r['note']} |")
@@ -975,6 +1068,8 @@ def main() -> int:
     ap.add_argument("--ops", action="store_true",
                     help="also time every op at its config shape (table on stderr)")
     ap.add_argument("--ops-only", action="store_true", help="only the per-op table")
+    ap.add_argument("--graph", action="store_true",
+                    help="per-op table: also time each op as a captured HIP graph replay")
     ap.add_argument("--ops-out", default=None, help="write the per-op table as JSON")
     ap.add_argument("--ops-table", metavar="OPS_JSON",
                     help="print the per-op markdown table of an --ops-out JSON; no GPU")
@@ -1002,6 +1097,9 @@ def main() -> int:
               "by rows / heads / experts with no exchange on the measured path.", file=sys.stderr)
         return 2
 
+    build_note = ""
+    if not a.no_cpu and a.op == "fused":
+        build_note = native_oracle()  # before any import of oracle.py in this process
     import torch
     import k3h
 
@@ -1011,7 +1109,7 @@ def main() -> int:
         print(ceilings_markdown(bench_ceilings(ctx, a.ceilings_out)), flush=True)
         return 0
     if a.ops_only:
-        bench_ops(ctx, max(5, a.steps), a.ops_out, 0.0 if a.no_cpu else 3.0)
+        bench_ops(ctx, max(5, a.steps), a.ops_out, 0.0 if a.no_cpu else 3.0, a.graph)
         return 0
     copy_gbs = copy_ceiling(ctx, rows, a.steps if a.op == "copy" else 20)
     if a.op == "copy":
@@ -1068,11 +1166,11 @@ def main() -> int:
             "avg_launch_us": round(ms * 1e3, 2), "copy_ceiling_gbs": round(copy_gbs, 1)}
     ops = None
     if a.ops:
-        ops = bench_ops(ctx, 50, a.ops_out, 0.0 if a.no_cpu else 3.0)
+        ops = bench_ops(ctx, 50, a.ops_out, 0.0 if a.no_cpu else 3.0, a.graph)
     cpu = None
     if not a.no_cpu:
         log("CPU baseline: C oracle on the same inputs")
-        cpu = cpu_baseline(x, res, gamma, (ro, q, sf), a.cpu_budget)
+        cpu = cpu_baseline(x, res, gamma, (ro, q, sf), a.cpu_budget, build_note)
         log(f"CPU {cpu['value']} GB/s on {cpu['cores']} threads; {cpu['sample']}")
     line = {
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1,

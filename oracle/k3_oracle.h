@@ -129,6 +129,7 @@ void k3o_situ_rms(const uint16_t* sp, uint16_t* act, const uint16_t* lat, const 
                   uint16_t* ln, int n, int B, int h, int L, int tokens);
 
 int k3o_num_threads(void);
+void k3o_par_copy(void* dst, const void* src, size_t n);
 
 /* ---- MoE expert GEMMs (k3_oracle_gemm.c) */
 float k3o_e2m1_decode(uint8_t nib);

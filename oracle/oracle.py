@@ -14,7 +14,9 @@ import subprocess
 import numpy as np
 
 ODIR = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(ODIR, "libk3oracle.so")
+# K3_ORACLE_LIB: another build of the same sources (bench.py's CPU baseline times a
+# build made with -march=native on the host it runs on)
+LIB_PATH = os.environ.get("K3_ORACLE_LIB") or os.path.join(ODIR, "libk3oracle.so")
 H = 7168
 
 _lib = None
@@ -162,11 +164,23 @@ def moe_quant(x, rows, cols):
     return q.reshape(rows, cols), sf.reshape(rows, cols // 32)
 
 
-def residual_rms_mxfp8(x, residual, gamma, B, eps=1e-6, want_normed=True):
-    res_out = np.empty((B, H), np.uint16)
-    q = np.empty((B, H), np.uint8)
-    sf = np.empty((B, H // 32), np.uint8)
-    normed = np.empty((B, H), np.uint16) if want_normed else None
+def par_copy(a):
+    """A copy of array a whose pages the OpenMP threads touch first."""
+    a = np.ascontiguousarray(a)
+    out = np.empty_like(a)
+    lib().k3o_par_copy(_p(out), _p(a), ctypes.c_size_t(a.nbytes))
+    return out
+
+
+def residual_rms_mxfp8(x, residual, gamma, B, eps=1e-6, want_normed=True, out=None):
+    """out: optional (res_out, q, sf, normed) arrays to write (allocated by the caller)."""
+    if out is not None:
+        res_out, q, sf, normed = out
+    else:
+        res_out = np.empty((B, H), np.uint16)
+        q = np.empty((B, H), np.uint8)
+        sf = np.empty((B, H // 32), np.uint8)
+        normed = np.empty((B, H), np.uint16) if want_normed else None
     lib().k3o_residual_rms_mxfp8(_p(x), _p(residual), _p(gamma), _p(res_out), _p(q), _p(sf),
                                  _p(normed), B, ctypes.c_float(eps))
     return res_out, q, sf, normed

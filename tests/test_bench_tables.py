@@ -85,6 +85,21 @@ def test_ops_markdown_columns(tmp_path):
     assert not any(l.startswith("| MoE fc2") and "629" in l for l in md)
 
 
+def test_ops_markdown_graph_columns(tmp_path):
+    ops = tmp_path / "ops.json"
+    rows = _ops_json(ops)
+    rows[1].update({"us_graph": 3.5, "gbs_graph": 898.6})
+    json.dump(rows, open(ops, "w"))
+    md = bench.ops_markdown(str(ops)).splitlines()
+    head = [c.strip() for c in md[0].strip("|").split("|")]
+    assert head[12] == "us, graph replay" and head[13] == "GB/s, graph replay"
+    assert all(l.count("|") == md[0].count("|") for l in md[:4])     # every row has the columns
+    cells = [c.strip() for c in next(l for l in md if l.startswith("| residual+")).strip("|").split("|")]
+    assert cells[12] == "3.50" and cells[13] == "898.6" and cells[14] == "2.0"
+    copy = [c.strip() for c in next(l for l in md if l.startswith("| stream copy")).strip("|").split("|")]
+    assert copy[12] == "" and copy[13] == ""                           # no graph figure: empty cells
+
+
 def test_ceilings_markdown_rates():
     rows = [
         {"probe": "copy_u4", "op": "copy", "loads_in_flight": 4, "grid": "flat 16", "cache": "non-temporal",
