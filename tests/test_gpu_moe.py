@@ -80,6 +80,31 @@ def test_router_topk_ties(ctx, topk):
     _eq("wts", wts.view(np.uint32), want_w.view(np.uint32))
 
 
+@pytest.mark.parametrize("topk", [8, 16])
+def test_router_topk_near_ties(ctx, topk):
+    """Rows whose largest logits lie a few ulps apart (and rows with an infinite
+    logit): the typed call ranks by the hardware logistic first, so
+    here its approximate order can differ from the exact one near the top-k
+    boundary; the exact keys must still decide the picks and their order."""
+    _case(f"router_topk near ties topk={topk}")
+    T = 95
+    g = rng(1770 + topk)
+    S = g.standard_normal((T, 224), dtype=np.float32)
+    for t in range(T - 3):
+        top = g.choice(224, size=topk + 4, replace=False)
+        base = np.float32(2.0 + g.random())
+        steps = g.integers(0, 4, topk + 4).astype(np.int32)  # 0-3 ulps apart, shuffled
+        S[t, top] = (base.view(np.int32) + steps).view(np.float32)
+    S[T - 3, 200] = np.inf
+    S[T - 2, 17] = -np.inf
+    bias = (g.standard_normal(224) * 1e-7).astype(np.float32)  # perturbations of a few ulps
+    rs = to_bf16(np.array([2.5], np.float32))
+    want_i, want_w = O.router_topk(S, bias, rs[0], T, topk)
+    idx, wts = _run_router(ctx, S, bias, rs, T, topk)
+    _eq("idx", idx, want_i)
+    _eq("wts", wts.view(np.uint32), want_w.view(np.uint32))
+
+
 def test_argmax_f32(ctx):
     _case("argmax")
     g = rng(1400)
