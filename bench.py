@@ -465,7 +465,8 @@ def _bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0, gr
     return rows
 
 
-def bench_ceilings(ctx, out_path: str | None, reps: int = 100, flushed_reps: int = 30) -> list:
+def bench_ceilings(ctx, out_path: str | None, reps: int = 100, flushed_reps: int = 30,
+                   only: str | None = None) -> list:
     """Ceilings of this GPU (module k3h_probe): HBM rates of read-only, write-only,
     copy and the fused op's 2-read : 1.5-write byte shape, over 235 MB streams,
     with 1 or 4 coalesced 16-byte loads in flight per lane (flat grids), 4 or 8
@@ -474,8 +475,12 @@ def bench_ceilings(ctx, out_path: str | None, reps: int = 100, flushed_reps: int
     at a time after a 512 MB clean-read flush (median of `flushed_reps`).  Then
     the register-to-register issue rate of v_mfma_scale_f32_32x32x64_f8f6f4 for
     e4m3 x e2m1 (the MoE GEMMs' operands), e4m3 x e4m3 and e2m1 x e2m1.  The
-    fused op and the operators' stream copy run in the same process."""
+    fused op and the operators' stream copy run in the same process.  `only`: a
+    regular expression; only the rows whose probe names match run (for counter
+    runs of a few shapes)."""
     import ctypes
+    import re
+    want = (lambda name: re.search(only, name) is not None) if only else (lambda name: True)
     import torch
     import k3h
     L = ctx.L
@@ -534,6 +539,8 @@ def bench_ceilings(ctx, out_path: str | None, reps: int = 100, flushed_reps: int
                 ("u4p", 4, 2048), ("u8p", 8, 2048), ("u4_c", 4, None)]
     for op, (nbytes, kinds, vals) in shapes.items():
         for suf, U, pgrid in variants:
+            if not want(f"{op}_{suf}"):
+                continue
             grid = pgrid or n16 // (256 * U)
             b2b, fl = time_it(launcher(f"k3h_probe_{op}_{suf}", grid, kinds, vals), reps, flushed_reps)
             row = {"probe": f"{op}_{suf}", "op": op, "loads_in_flight": U,
@@ -547,24 +554,31 @@ def bench_ceilings(ctx, out_path: str | None, reps: int = 100, flushed_reps: int
     # the operators' copy and the fused op, same process
     ta = a.view(torch.bfloat16)
     tc = c.view(torch.bfloat16)
-    b2b, fl = time_it(lambda: ctx.stream_copy(ta, tc, stream=s), reps, flushed_reps)
-    rows.append({"probe": "k3h_stream_copy (operators' module)", "op": "copy", "loads_in_flight": 1,
-                 "grid": f"flat {n16 // 256}", "cache": "non-temporal", "bytes": 32 * n16,
-                 "us_b2b": round(b2b, 2), "gbs_b2b": round(32 * n16 / b2b / 1e3, 1),
-                 "us_flushed": round(fl, 2), "gbs_flushed": round(32 * n16 / fl / 1e3, 1)})
+    if want("k3h_stream_copy"):
+        b2b, fl = time_it(lambda: ctx.stream_copy(ta, tc, stream=s), reps, flushed_reps)
+        rows.append({"probe": "k3h_stream_copy (operators' module)", "op": "copy", "loads_in_flight": 1,
+                     "grid": f"flat {n16 // 256}", "cache": "non-temporal", "bytes": 32 * n16,
+                     "us_b2b": round(b2b, 2), "gbs_b2b": round(32 * n16 / b2b / 1e3, 1),
+                     "us_flushed": round(fl, 2), "gbs_flushed": round(32 * n16 / fl / 1e3, 1)})
     del a, b, c, d
     x, res, gm = make_inputs(T)
     ro = torch.empty_like(x)
     q = torch.empty((T, H), dtype=torch.uint8, device="cuda")
     sf = torch.empty((T, H // 32), dtype=torch.uint8, device="cuda")
     nb = algo_bytes(T)
-    b2b, fl = time_it(lambda: ctx.residual_rms_mxfp8(x, res, gm, ro, q, sf, None, eps=1e-6, B=T,
-                                                     stream=s), reps, flushed_reps)
-    rows.append({"probe": "k3h_residual_rms_mxfp8 (the fused op)", "op": "shape", "loads_in_flight": 14,
-                 "grid": f"flat {T // 2}", "cache": "non-temporal", "bytes": nb,
-                 "us_b2b": round(b2b, 2), "gbs_b2b": round(nb / b2b / 1e3, 1),
-                 "us_flushed": round(fl, 2), "gbs_flushed": round(nb / fl / 1e3, 1)})
+    if want("k3h_residual_rms_mxfp8"):
+        b2b, fl = time_it(lambda: ctx.residual_rms_mxfp8(x, res, gm, ro, q, sf, None, eps=1e-6, B=T,
+                                                         stream=s), reps, flushed_reps)
+        rows.append({"probe": "k3h_residual_rms_mxfp8 (the fused op)", "op": "shape", "loads_in_flight": 14,
+                     "grid": f"flat {T // 2}", "cache": "non-temporal", "bytes": nb,
+                     "us_b2b": round(b2b, 2), "gbs_b2b": round(nb / b2b / 1e3, 1),
+                     "us_flushed": round(fl, 2), "gbs_flushed": round(nb / fl / 1e3, 1)})
     del x, res, gm, ro, q, sf
+    if only:  # the operator-shape and MFMA rows are not filtered: a filtered run stops here
+        if out_path:
+            with open(out_path, "w") as f:
+                json.dump(rows, f, indent=1)
+        return rows
     rows += bench_op_shapes(ctx, launcher, time_it, reps, flushed_reps)
     # MFMA issue rate, register operands
     n_wg, iters = 256 * 2, 2000
@@ -1063,6 +1077,8 @@ def main() -> int:
                     help="copy: only the 16-byte streaming copy (counter calibration); "
                          "ceilings: HBM access-shape and MFMA-rate probes (markdown on stdout)")
     ap.add_argument("--ceilings-out", default=None, help="write the ceilings rows as JSON")
+    ap.add_argument("--probe-filter", default=None,
+                    help="--op ceilings: a regular expression; only the probes whose names match run")
     ap.add_argument("--ceilings-table", metavar="CEILINGS_JSON",
                     help="print the markdown table of a --ceilings-out JSON; no GPU")
     ap.add_argument("--ops", action="store_true",
@@ -1106,7 +1122,7 @@ def main() -> int:
     ctx = k3h.Ctx()
     rows = a.rows
     if a.op == "ceilings":
-        print(ceilings_markdown(bench_ceilings(ctx, a.ceilings_out)), flush=True)
+        print(ceilings_markdown(bench_ceilings(ctx, a.ceilings_out, only=a.probe_filter)), flush=True)
         return 0
     if a.ops_only:
         bench_ops(ctx, max(5, a.steps), a.ops_out, 0.0 if a.no_cpu else 3.0, a.graph)
