@@ -601,9 +601,10 @@ def bench_op_shapes(ctx, launcher, time_it, reps: int, flushed_reps: int) -> lis
     """The operator-shape probes of k3h_probe next to the operators they mirror,
     in one process on the same inputs' shapes: the KDA span gather (cfg 3a: 3-row
     re-read per 16 or per 32 rows, or none), the weighted finalize (cfg 5d: rows
-    gathered through the config-5 routing's exp2perm, one row written per token)
-    and the MXFP8 permute's payload (cfg 5c: one row gathered per padded row).
-    Each probe's bytes are its own algorithmic bytes (re-reads not counted);
+    gathered through the config-5 routing's exp2perm, one row written per token),
+    the MXFP8 permute's payload (cfg 5c: one row gathered per padded row) and the
+    residual push v3 at nb 0 (one row read, five written, at 128 or 896 threads
+    per row).  Each probe's bytes are its own algorithmic bytes (re-reads not counted);
     the operator rows carry the operators' algorithmic bytes."""
     import torch
     s = torch.cuda.current_stream()
@@ -673,6 +674,24 @@ def bench_op_shapes(ctx, launcher, time_it, reps: int, flushed_reps: int) -> lis
                  [x8, rmap, pq, tpad, H]), f"flat {-(-tpad // 4)} x 256", "non-temporal, one row per wave")
     row("k3h_moe_permute_mx (the operator, cfg 5c)", "permute", 2 * tpad * (H + H // 32),
         lambda: ctx.moe_permute_mx(x8, sf8, rmap, tp, H, pq, psf, stream=s), "typed call", "non-temporal")
+    del x8, sf8, pq, psf
+    # residual push v3 at nb 0, 4 ranks (the per-op table's (f)1 row): one row
+    # read, the snapshot slot and four normed copies written
+    B = T // 4
+    prefix = syn("f1/prefix", (B, H))
+    blocks = torch.empty((B, 8, H), dtype=torch.bfloat16, device="cuda")
+    normed = [torch.empty((4 * B, H), dtype=torch.bfloat16, device="cuda") for _ in range(4)]
+    peer = torch.tensor([t.data_ptr() for t in normed], dtype=torch.int64, device="cuda")
+    gm = syn("f1/gamma", (H,), mean=1.0, std=0.1)
+    sw = torch.zeros(H, dtype=torch.float32, device="cuda")
+    P7 = ["in buffer<bf16>"] + ["out buffer<bf16>"] * 5 + ["i32"]
+    for nt in (128, 896):
+        row(f"push_t{nt}", "push shape", 6 * B * H * 2,
+            launcher(f"k3h_probe_push_t{nt}", B, P7, [prefix, blocks, *normed, B], block=nt),
+            f"flat {B} x {nt}", f"non-temporal, {7168 // 8 // nt} vectors per lane, 1 row read : 5 written")
+    row("kern_k3_attnres_rms_push (the operator, push v3 nb 0)", "push", 6 * B * H * 2 + H * 2,
+        lambda: ctx.attnres_rms_push(prefix, blocks, sw, gm, normed[1], peer, 0, 1, B, 1, 4, version=3,
+                                     stream=s), "typed call", "non-temporal")
     return out
 
 

@@ -233,6 +233,13 @@ K3_DEV void k3_st16(void* p, k3_u4 v) { *(k3_u4*)p = v; }
 K3_DEV k3_u4 k3_ld16_nt(const void* p) { return __builtin_nontemporal_load((const k3_u4*)p); }
 K3_DEV void k3_st16_nt(void* p, k3_u4 v) { __builtin_nontemporal_store(v, (k3_u4*)p); }
 K3_DEV void k3_st8_nt(void* p, k3_u2 v) { __builtin_nontemporal_store(v, (k3_u2*)p); }
+// Non-temporal store through an address read from memory (a peer rank's
+// buffer): cast to the global address space, so it is issued as a global store
+// and counts only in the vector memory counter.  Through the generic pointer it
+// would be a flat store, which also counts in the counter that scalar loads
+// wait on, so the wait for the next peer address would wait for the store.
+typedef __attribute__((address_space(1))) k3_u4 k3_gu4;
+K3_DEV void k3_st16_nt_g(void* p, k3_u4 v) { __builtin_nontemporal_store(v, (k3_gu4*)p); }
 K3_DEV float4 k3_ld16f_nt(const float* p) {
   const k3_u4 u = k3_ld16_nt(p);
   return make_float4(__uint_as_float(u[0]), __uint_as_float(u[1]), __uint_as_float(u[2]), __uint_as_float(u[3]));

@@ -3,8 +3,9 @@
 // land_add2 fold), plus res_mlp's statistics-consuming nb entries.  One
 // workgroup per row, grid ceil_div(tokens, 4) = B rows per rank as the manifest's
 // (k3-tp4-prefill-16k.json:406806 attnres_rms_push_first_v3, 407299
-// attnres_rms_push_add2, 406999 land_add_attnres_rms_bf16_v2_nb4): 128 threads
-// at nb 0 (the manifest entry), 256 threads (the vector-split entries) at nb >= 1.
+// attnres_rms_push_add2, 406999 land_add_attnres_rms_bf16_v2_nb4): 896 threads
+// at nb 0, 256 threads (the vector-split entries) at nb >= 1; the manifest's
+// 128-thread entry serves the module-layer launch.
 #include <string>
 
 #include "k3h_internal.h"
@@ -14,6 +15,7 @@ namespace {
 constexpr int kNbMax = 8;
 constexpr int kMaxRanks = 8;
 constexpr uint32_t kResThreads = 128;
+constexpr uint32_t kWideThreads = 896;
 
 // Checks shared by the push entries; dst_peer is read only for q < nranks, q != rank.
 int check_push(const void* blocks, const float* sw, const void* gamma, const void* normed_all,
@@ -29,13 +31,15 @@ int check_push(const void* blocks, const float* sw, const void* gamma, const voi
   return K3H_OK;
 }
 
-// 1 <= nb <= kSplitNbMax: the module's 256-thread vector-split entry for that nb
-// (same parameter list and outputs); otherwise the 128-thread entry.
+// nb == 0: the module's 896-thread entry (one 16-byte vector of the row per
+// lane); 1 <= nb <= kSplitNbMax: its 256-thread vector-split entry for that nb;
+// otherwise the 128-thread manifest entry.  Same parameter list and outputs.
 struct PushEntry {
   std::string name;
   uint32_t threads;
 };
 PushEntry push_entry(int nb) {
+  if (nb == 0) return {"k3h_attnres_rms_push_nb0w896", kWideThreads};
   if (nb >= 1 && nb <= kSplitNbMax)
     return {"k3h_attnres_rms_push_nb" + std::to_string(nb) + "s", kSplitThreads};
   return {"kern_k3_attnres_rms_push", kResThreads};

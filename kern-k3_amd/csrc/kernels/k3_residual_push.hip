@@ -41,8 +41,8 @@
 #define K3_PUSH_EPS 1e-5f
 
 #if K3_PUSH == 3
-// hidden = bf16(f32(prefix2) + f32(p1) [+ f32(p2)]) for this thread's vectors.
-// hidden = bf16(f32(prefix2) + f32(p1) [+ f32(p2)]), left to right, one rounding
+// hidden = bf16(f32(prefix2) + f32(p1) [+ f32(p2)]) for this thread's vectors,
+// left to right, one rounding
 K3_DEV k3_u4 k3_add2_vec(k3_u4 pv, k3_u4 a, k3_u4 e, int two) {
   k3_u4 o;
 #pragma unroll
@@ -157,7 +157,7 @@ extern "C" __global__ void __launch_bounds__(K3_RES_THREADS) kern_k3_attnres_rms
         if (q == rank) continue;
         uint16_t* prow = (uint16_t*)(uintptr_t)dst_peer[q] + dst_off;
 #pragma unroll
-        for (int v = 0; v < K3_KVPT; ++v) k3_st16_nt(prow + k3_vec_off(t, v), nv[v]);
+        for (int v = 0; v < K3_KVPT; ++v) k3_st16_nt_g(prow + k3_vec_off(t, v), nv[v]);
       }
     }
     return;
@@ -184,6 +184,114 @@ extern "C" __global__ void __launch_bounds__(K3_RES_THREADS) kern_k3_attnres_rms
   k3_attnres_rms_row_to<-1>(blocks + (size_t)b * K3_NB_MAX * K3_H, pv, sw, gamma, dst, nb,
                             K3_PUSH_EPS, t);
 #endif
+}
+
+// ---------------------------------------------------------------- nb 0, wide
+// Typed-call entry k3h_attnres_rms_push_nb0w896 for nb == 0 (the module's
+// parameter list; block 896, grid B): lane `tid` owns the row's vector tid, so
+// each lane has one store per destination in flight.  The row goes through LDS
+// once: lanes 0-127 replay the per-thread sums of squares in the K1 ownership
+// (thread t: vectors t + 128 v, v = 0..6, one fma chain) and the half-wave
+// partials in order, so r has the bits of the 128-thread body.  gamma is
+// loaded ahead of the row, so the one wait for the row covers it, and the
+// snapshot slot (and, for push_add2, `hidden`) is stored before the reduction.
+// Measured at B 4096, 4 ranks (every normed copy local), back to back over 4
+// rotating sets of buffers: 56.1 us (6.28 TB/s) against 69.2 for the module
+// entry's 128-thread body, 60.1 with the snapshot stored after the reduction,
+// 66.9 at 448 threads (2 vectors per lane); the same byte shape with no
+// arithmetic runs 53.2 us at 896 threads and 71.2 at 128.
+template <int NT>
+K3_DEV void k3w_push_nb0(
+#if K3_PUSH != 3
+    const uint16_t* __restrict__ prefix,
+#endif
+    uint16_t* __restrict__ blocks, const uint16_t* __restrict__ gamma,
+    uint16_t* __restrict__ normed_all, const unsigned long long* __restrict__ dst_peer,
+    int snapshot, int B, int rank, int nranks
+#if K3_PUSH == 3
+    , const uint16_t* __restrict__ p1, const uint16_t* __restrict__ p2,
+    const uint16_t* __restrict__ prefix2, uint16_t* __restrict__ hidden, int two
+#endif
+) {
+  constexpr int NV = 896 / NT;
+  static_assert(NV * NT == 896 && NT >= K3_RES_THREADS, "NT divides the row's 896 vectors");
+  __shared__ k3_u4 s_row[896];
+  __shared__ float s_red[K3_NHW];
+  const int b = blockIdx.x;
+  if (b >= B) return;
+  const int tid = threadIdx.x;
+  const int nr = nranks < K3_MAX_RANKS ? nranks : K3_MAX_RANKS;
+  const long long dst_off = ((long long)rank * B + b) * K3_H;
+  const size_t row = (size_t)b * K3_H;
+  k3_u4 pv[NV], g[NV];
+  // gamma first: the wait for the row's own loads then covers it, and no
+  // store issued after that wait is waited for again
+#pragma unroll
+  for (int v = 0; v < NV; ++v) g[v] = k3_ld16(gamma + (tid + NT * v) * 8);
+  __builtin_amdgcn_sched_barrier(0);
+#if K3_PUSH == 3
+  k3_u4 a[NV], e[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    a[v] = k3_ld16_nt(p1 + row + (tid + NT * v) * 8);
+    pv[v] = k3_ld16_nt(prefix2 + row + (tid + NT * v) * 8);
+  }
+  if (two) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) e[v] = k3_ld16_nt(p2 + row + (tid + NT * v) * 8);
+  }
+#else
+#pragma unroll
+  for (int v = 0; v < NV; ++v) pv[v] = k3_ld16_nt(prefix + row + (tid + NT * v) * 8);
+#endif
+#if K3_PUSH == 3
+#pragma unroll
+  for (int v = 0; v < NV; ++v) pv[v] = k3_add2_vec(pv[v], a[v], e[v], two);
+#endif
+#pragma unroll
+  for (int v = 0; v < NV; ++v) s_row[tid + NT * v] = pv[v];
+  // the rows that need neither r nor gamma leave before the reduction
+  uint16_t* snap = snapshot ? blocks + (size_t)b * K3_NB_MAX * K3_H : nullptr;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+#if K3_PUSH == 3
+    k3_st16(hidden + row + (tid + NT * v) * 8, pv[v]);
+#endif
+    if (snap) k3_st16_nt(snap + (tid + NT * v) * 8, pv[v]);
+  }
+  __syncthreads();
+  if (tid < K3_RES_THREADS) {
+    k3_u4 kv[K3_KVPT];
+#pragma unroll
+    for (int v = 0; v < K3_KVPT; ++v) kv[v] = s_row[tid + K3_RES_THREADS * v];
+    const float part = k3_sum32(k3_row_sumsq(kv));
+    if ((tid & 31) == 0) s_red[tid >> 5] = part;
+  }
+  __syncthreads();
+  float tot = 0.0f;
+#pragma unroll
+  for (int w = 0; w < K3_NHW; ++w) tot += s_red[w];
+  const float r = k3_row_rscale(tot, K3_PUSH_EPS);
+  uint16_t* lrow = normed_all + dst_off;
+  k3_u4 nv[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      nv[v][j] = k3_mul_bf2(k3_pack_bf2(k3_bf_lo(pv[v][j]) * r, k3_bf_hi(pv[v][j]) * r), g[v][j]);
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int u = (tid + NT * v) * 8;
+    k3_st16_nt(lrow + u, nv[v]);
+    if (dst_peer) {
+#pragma unroll
+      for (int q = 0; q < K3_MAX_RANKS; ++q) {
+        if (q >= nr) break;
+        if (q == rank) continue;
+        k3_st16_nt_g((uint16_t*)(uintptr_t)dst_peer[q] + dst_off + u, nv[v]);
+      }
+    }
+  }
 }
 
 // ---------------------------------------------------------------- split form
@@ -296,3 +404,15 @@ K3P_SPLIT_ENTRY(5)
 K3P_SPLIT_ENTRY(6)
 K3P_SPLIT_ENTRY(7)
 K3P_SPLIT_ENTRY(8)
+
+#if K3_PUSH == 3
+#define K3W_ARGS blocks, gamma, normed_all, dst_peer, snapshot, B, rank, nranks, p1, p2, prefix2, hidden, two
+#else
+#define K3W_ARGS prefix, blocks, gamma, normed_all, dst_peer, snapshot, B, rank, nranks
+#endif
+#define K3W_ENTRY(NT)                                                                         \
+  extern "C" __global__ void __launch_bounds__(NT) k3h_attnres_rms_push_nb0w##NT(K3P_PARAMS) { \
+    (void)nb; (void)sw;                                                                       \
+    k3w_push_nb0<NT>(K3W_ARGS);                                                               \
+  }
+K3W_ENTRY(896)

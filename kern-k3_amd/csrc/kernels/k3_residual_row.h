@@ -402,7 +402,7 @@ K3_DEV void k3_attnres_rms_row_to(const uint16_t* __restrict__ blk_row, k3_u4* p
       if (q == dst.rank) continue;
       uint16_t* prow = (uint16_t*)(uintptr_t)dst.peer[q] + dst.off;
 #pragma unroll
-      for (int v = 0; v < K3_KVPT; ++v) k3_st16_nt(prow + k3_vec_off(t, v), nv[v]);
+      for (int v = 0; v < K3_KVPT; ++v) k3_st16_nt_g(prow + k3_vec_off(t, v), nv[v]);
     }
   }
 }

@@ -333,7 +333,7 @@ K3_DEV void k3s_attnres_rms_row(k3_u4 (&xc)[NB][K3S_SLOTS], k3_u4* pv,
       uint16_t* prow = (uint16_t*)(uintptr_t)dst.peer[q] + dst.off;
 #pragma unroll
       for (int s = 0; s < K3S_SLOTS; ++s)
-        if (L.valid(s)) k3_st16_nt(prow + L.off(s), nv[s]);
+        if (L.valid(s)) k3_st16_nt_g(prow + L.off(s), nv[s]);
     }
   }
 }

@@ -36,6 +36,9 @@
 //   k3h_probe_rowgather(src, idx, dst, R, cols)   the MXFP8 permute's payload:
 //       dst[r] = src[idx[r]] (cols bytes, cols % 1024 == 0), one wave per row,
 //       4 rows per 256-thread workgroup, all of a row's loads before its stores.
+//   k3h_probe_push_t<NT>(src, snap, n0, n1, n2, n3, B)   the nb-0 residual push
+//       at 4 ranks: one row read, five written (the snapshot slot and four
+//       normed copies), grid B, NT = 128 (7 vectors per lane) or 896 (1).
 //
 // MFMA probe: k3h_probe_mfma_<A><B>(out, iters), block 256, any grid: each
 // wave issues iters x 4 independent v_mfma_scale_f32_32x32x64_f8f6f4 on
@@ -253,6 +256,40 @@ extern "C" __global__ void __launch_bounds__(256) k3h_probe_rowgather(
       if (v0 + lane + 64 * j < nvec) __builtin_nontemporal_store(x[j], d + v0 + lane + 64 * j);
   }
 }
+
+// The nb-0 residual push at 4 ranks: row b of src (one 14,336-byte row) is
+// stored to snap[8 b] (the snapshot slot's row stride) and to row B + b of each
+// of n0..n3 (rank 1's rows of four normed_all buffers).  NT threads per row, each
+// 7168 / (8 NT) vectors; every load first, then each vector to all five
+// destinations.  NT = 128 is the operator's layout, NT = 896 one vector (one
+// store per destination) per lane.
+template <int NT>
+K3_DEV void kp_push(const k3_u4* __restrict__ src, k3_u4* __restrict__ snap, k3_u4* __restrict__ n0,
+                    k3_u4* __restrict__ n1, k3_u4* __restrict__ n2, k3_u4* __restrict__ n3, int B) {
+  constexpr int RV = 7168 / 8, NV = RV / NT;
+  const int b = blockIdx.x, t = threadIdx.x;
+  if (b >= B) return;
+  k3_u4 x[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) x[v] = __builtin_nontemporal_load(src + (size_t)b * RV + t + NT * v);
+  const size_t o = (size_t)(B + b) * RV;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int u = t + NT * v;
+    __builtin_nontemporal_store(x[v], snap + (size_t)b * 8 * RV + u);
+    __builtin_nontemporal_store(x[v], n0 + o + u);
+    __builtin_nontemporal_store(x[v], n1 + o + u);
+    __builtin_nontemporal_store(x[v], n2 + o + u);
+    __builtin_nontemporal_store(x[v], n3 + o + u);
+  }
+}
+#define KP_PUSH(NT)                                                                            \
+  extern "C" __global__ void __launch_bounds__(NT) k3h_probe_push_t##NT(                       \
+      const k3_u4* src, k3_u4* snap, k3_u4* n0, k3_u4* n1, k3_u4* n2, k3_u4* n3, int B) {      \
+    kp_push<NT>(src, snap, n0, n1, n2, n3, B);                                                 \
+  }
+KP_PUSH(128)
+KP_PUSH(896)
 
 // ---------------------------------------------------------------- MFMA rate
 template <int FA, int FB>

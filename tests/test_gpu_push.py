@@ -62,7 +62,8 @@ class Ranks:
 
 @pytest.mark.parametrize("version", [1, 3])
 @pytest.mark.parametrize("nb,snapshot,B,rank,nranks", [
-    (0, 1, 37, 1, 4),     # the manifest's first-layer call (nb 0, snapshot 1)
+    (0, 1, 37, 1, 4),     # the manifest's first-layer call (nb 0, snapshot 1): the 896-thread entry
+    (0, 0, 5, 0, 1),      # nb 0, one rank, no snapshot
     (3, 0, 16, 0, 4),
     (8, 1, 9, 3, 4),      # nb = 8: no snapshot slot left
     (2, 1, 5, 0, 1),      # one rank: no peers read
@@ -188,7 +189,7 @@ def test_push_full_rank_share(ctx):
     _eq("blocks[:, 0]", from_dev(blocks)[:, 0], prefix)
 
 
-@pytest.mark.parametrize("nb", [4, 8])
+@pytest.mark.parametrize("nb", [0, 4, 8])
 def test_push_add2_full_rank_share(ctx, nb):
     """push_add2 at one rank's share of the 16k prefill (B = 4096 rows, the
     benchmarked shape), every row bit-exact: hidden, every rank's normed copy,
