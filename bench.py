@@ -689,7 +689,7 @@ def bench_op_shapes(ctx, launcher, time_it, reps: int, flushed_reps: int) -> lis
         row(f"push_t{nt}", "push shape", 6 * B * H * 2,
             launcher(f"k3h_probe_push_t{nt}", B, P7, [prefix, blocks, *normed, B], block=nt),
             f"flat {B} x {nt}", f"non-temporal, {7168 // 8 // nt} vectors per lane, 1 row read : 5 written")
-    row("kern_k3_attnres_rms_push (the operator, push v3 nb 0)", "push", 6 * B * H * 2 + H * 2,
+    row("k3h_attnres_rms_push_nb0w896 (the operator, push v3 nb 0)", "push", 6 * B * H * 2 + H * 2,
         lambda: ctx.attnres_rms_push(prefix, blocks, sw, gm, normed[1], peer, 0, 1, B, 1, 4, version=3,
                                      stream=s), "typed call", "non-temporal")
     return out
@@ -740,7 +740,7 @@ def bench_push_land(ctx, add, timed, bf, g, s, O=None, h=None) -> None:
     blocks = bf(B, 8, HH)
     normed = [torch.empty((4 * B, HH), dtype=torch.bfloat16, device="cuda") for _ in range(4)]
     peer = torch.tensor([t.data_ptr() for t in normed], dtype=torch.int64, device="cuda")
-    add("residual push v3 (res_in, nb 0, 4 ranks)", "kern_k3_attnres_rms_push", f"B={B} nb=0",
+    add("residual push v3 (res_in, nb 0, 4 ranks)", "k3h_attnres_rms_push_nb0w896", f"B={B} nb=0",
         row + HH * 2 + row + 4 * row,
         timed(lambda: ctx.attnres_rms_push(prefix, blocks, sw, gm, normed[1], peer, 0, 1, B, 1, 4,
                                            version=3, stream=s)))
@@ -870,7 +870,7 @@ OP_KERNELS = {
     "EP routing, one launch (k3h_moe_route)": ["k3h_moe_route_fused"],
     "MXFP8 permute (cfg 5c)": ["k3h_moe_permute_mx"],
     "weighted finalize (cfg 5d)": ["k3h_moe_finalize_rows"],
-    "residual push v3 (res_in, nb 0, 4 ranks)": ["kern_k3_attnres_rms_push"],
+    "residual push v3 (res_in, nb 0, 4 ranks)": ["k3h_attnres_rms_push_nb0w896"],
     "residual push_add2 (res_in, nb 4, 4 ranks)": ["k3h_attnres_rms_push_nb4s"],
     "K1b nb 1 (res_mlp, typed call)": ["k3h_land_add_attnres_rms_nb1s"],
     "K1b nb 4 (res_mlp, typed call)": ["k3h_land_add_attnres_rms_nb4s"],
