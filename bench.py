@@ -688,7 +688,7 @@ def bench_op_shapes(ctx, launcher, time_it, reps: int, flushed_reps: int) -> lis
     for nt in (128, 896):
         row(f"push_t{nt}", "push shape", 6 * B * H * 2,
             launcher(f"k3h_probe_push_t{nt}", B, P7, [prefix, blocks, *normed, B], block=nt),
-            f"flat {B} x {nt}", f"non-temporal, {7168 // 8 // nt} vectors per lane, 1 row read : 5 written")
+            f"flat {B} x {nt}", f"non-temporal, {7168 // 8 // nt} vector{'s' if nt < 896 else ''} per lane, 1 row read : 5 written")
     row("k3h_attnres_rms_push_nb0w896 (the operator, push v3 nb 0)", "push", 6 * B * H * 2 + H * 2,
         lambda: ctx.attnres_rms_push(prefix, blocks, sw, gm, normed[1], peer, 0, 1, B, 1, 4, version=3,
                                      stream=s), "typed call", "non-temporal")
