@@ -337,10 +337,6 @@ K3_DEV void k3s_push_body(
 #endif
   k3_u4 xc[NB][K3S_SLOTS];
   k3s_load_candidates<NB>(xc, blocks + (size_t)b * K3_NB_MAX * K3_H, L);
-#if K3_PUSH == 3
-#pragma unroll
-  for (int s = 0; s < K3S_SLOTS; ++s) pv[s] = k3_add2_vec(pv[s], a[s], e[s], two);
-#endif
   // hidden (K3_PUSH 3) and the snapshot slot are stored by the row body once
   // its own loads are out
   const K3NormedDst dst = {normed_all + dst_off, dst_peer, dst_off, rank, nr};
@@ -352,7 +348,16 @@ K3_DEV void k3s_push_body(
 #endif
       snapshot && NB < K3_NB_MAX ? blocks + ((size_t)b * K3_NB_MAX + NB) * K3_H : nullptr,
       nullptr};
-#if K3_PUSH >= 2
+#if K3_PUSH == 3
+  // the land_add2 sum runs after the body has issued its own loads (measured
+  // equal to running it first, nb 4 at B 4096)
+  k3s_attnres_rms_row<NB, K3_MIX_STATS_OUT>(xc, pv, sw, gamma, dst, pvst, K3_PUSH_EPS, L, nullptr,
+                                             0, sw_mlp, stats + (size_t)b * K3_NB_MAX * 2,
+                                             [&](k3_u4* p) {
+#pragma unroll
+    for (int s = 0; s < K3S_SLOTS; ++s) p[s] = k3_add2_vec(p[s], a[s], e[s], two);
+  });
+#elif K3_PUSH == 2
   k3s_attnres_rms_row<NB, K3_MIX_STATS_OUT>(xc, pv, sw, gamma, dst, pvst, K3_PUSH_EPS, L, nullptr,
                                              0, sw_mlp, stats + (size_t)b * K3_NB_MAX * 2);
 #else

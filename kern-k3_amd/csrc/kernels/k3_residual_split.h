@@ -122,13 +122,21 @@ K3_DEV void k3s_load_candidates(k3_u4 (&xc)[NB][K3S_SLOTS], const uint16_t* __re
 // stats_out[c] = (sq_c, dm_c) is written (the 128-thread body's half-wave-0 totals:
 // the four per-wave partials summed in wave order).  The normed row goes to every
 // destination of `dst` (the local row and, for the push entries, each peer's).
-template <int NB, int MODE>
+// No step between the row body's own loads and its first use of pv.
+struct K3sNoPre {
+  K3_DEV void operator()(k3_u4*) const {}
+};
+
+// pre(pv) runs once the body's own loads (sw, sw_mlp, gamma) are issued: the
+// callers that form the prefix row from landing operands do it there, so that
+// those loads do not wait behind the operands' arrival.
+template <int NB, int MODE, class Pre = K3sNoPre>
 K3_DEV void k3s_attnres_rms_row(k3_u4 (&xc)[NB][K3S_SLOTS], k3_u4* pv,
                                 const float* __restrict__ sw, const uint16_t* __restrict__ gamma,
                                 const K3NormedDst& dst, const K3sPvStores& pvst, float eps,
                                 const K3sLane& L, const float* __restrict__ stats_in,
                                 int nb_stats, const float* __restrict__ sw_mlp = nullptr,
-                                float* __restrict__ stats_out = nullptr) {
+                                float* __restrict__ stats_out = nullptr, Pre pre = Pre()) {
   static_assert(NB >= 1 && NB <= K3_NB_MAX, "NB in 1..8");
   constexpr bool SIN = (MODE & K3_MIX_STATS_IN) != 0;
   constexpr bool SOUT = (MODE & K3_MIX_STATS_OUT) != 0;
@@ -157,6 +165,7 @@ K3_DEV void k3s_attnres_rms_row(k3_u4 (&xc)[NB][K3S_SLOTS], k3_u4* pv,
 #pragma unroll
     for (int s = 0; s < K3S_SLOTS; ++s) gv[s] = k3_ld16(gamma + L.off(s));
   }
+  pre(pv);
 #pragma unroll
   for (int s = 0; s < K3S_SLOTS; ++s) {
     if (!L.valid(s)) continue;
@@ -364,14 +373,27 @@ K3_DEV void k3s_land_add_attnres_rms_body(const k3_land_t* __restrict__ partial,
   }
   k3_u4 xc[NB][K3S_SLOTS];
   k3s_load_candidates<NB>(xc, blocks + (size_t)b * K3_NB_MAX * K3_H, L);
-  if (!snapshot) {
-#pragma unroll
-    for (int s = 0; s < K3S_SLOTS; ++s) pv[s] = k3_add_land(pr[s], pv[s]);
-  }
   const bool have_stats = MODE != 0 && stats != nullptr;
   const K3NormedDst dst = {normed + row, nullptr, 0, 0, 1};
   const K3sPvStores pvst = {nullptr, prefix2 + row, nullptr};
-  k3s_attnres_rms_row<NB, MODE>(xc, pv, sw, gamma, dst, pvst, K3_EPS, L,
-                                have_stats ? stats + (size_t)b * K3_NB_MAX * 2 : nullptr,
-                                have_stats ? nb_stats : 0);
+  auto land = [&](k3_u4* p) {
+    if (!snapshot) {
+#pragma unroll
+      for (int s = 0; s < K3S_SLOTS; ++s) p[s] = k3_add_land(pr[s], p[s]);
+    }
+  };
+  // From nb 2 the landing add runs after the body has issued its own loads (sw,
+  // gamma), which then do not wait for the landing operands (B 4096, back to
+  // back: nb 4 / 6 / 8 82.1 / 106.5 / 127.6 -> 80.9 / 103.1 / 124.9 us, identical
+  // outputs); at nb 1 the extra live registers cost a wave per SIMD (93 -> 105)
+  // and it measured 0.5-1.5% slower, so the add stays ahead there.
+  const float* st = have_stats ? stats + (size_t)b * K3_NB_MAX * 2 : nullptr;
+  const int ns = have_stats ? nb_stats : 0;
+  if constexpr (NB == 1) {
+    land(pv);
+    k3s_attnres_rms_row<NB, MODE>(xc, pv, sw, gamma, dst, pvst, K3_EPS, L, st, ns);
+  } else {
+    k3s_attnres_rms_row<NB, MODE>(xc, pv, sw, gamma, dst, pvst, K3_EPS, L, st, ns, nullptr,
+                                  nullptr, land);
+  }
 }
