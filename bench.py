@@ -602,8 +602,8 @@ def bench_op_shapes(ctx, launcher, time_it, reps: int, flushed_reps: int) -> lis
     in one process on the same inputs' shapes: the KDA span gather (cfg 3a: 3-row
     re-read per 16 or per 32 rows, or none), the weighted finalize (cfg 5d: rows
     gathered through the config-5 routing's exp2perm, one row written per token),
-    the MXFP8 permute's payload (cfg 5c: one row gathered per padded row) and the
-    residual push v3 at nb 0 (one row read, five written, at 128 or 896 threads
+    the MXFP8 permute's payload (cfg 5c: one row gathered per padded row), the MLA
+    RoPE pack (cfg 4: one wave per token) and the residual push v3 at nb 0 (one row read, five written, at 128 or 896 threads
     per row).  Each probe's bytes are its own algorithmic bytes (re-reads not counted);
     the operator rows carry the operators' algorithmic bytes."""
     import torch
@@ -675,6 +675,20 @@ def bench_op_shapes(ctx, launcher, time_it, reps: int, flushed_reps: int) -> lis
     row("k3h_moe_permute_mx (the operator, cfg 5c)", "permute", 2 * tpad * (H + H // 32),
         lambda: ctx.moe_permute_mx(x8, sf8, rmap, tp, H, pq, psf, stream=s), "typed call", "non-temporal")
     del x8, sf8, pq, psf
+    # MLA latent norm + RoPE + q pack (cfg 4): one wave per token
+    lat, kr, qq = syn("4/latent", (T, 512)), syn("4/k_rope", (T, 64)), syn("4/q", (T, 16, 192))
+    gk = syn("4/gamma_kv", (512,), 1.0, 0.1)
+    pos = torch.arange(T, dtype=torch.int64, device="cuda")
+    lo = torch.empty((T, 576), dtype=torch.bfloat16, device="cuda")
+    qo = torch.empty_like(qq)
+    rope_bytes = T * (512 + 64 + 16 * 192) * 2 + T * (576 + 16 * 192) * 2
+    row("rope", "RoPE pack shape", rope_bytes,
+        launcher("k3h_probe_rope", -(-T // 4), ["in buffer<bf16>"] * 3 + ["out buffer<bf16>"] * 2 + ["i32", "i32"],
+                 [lat, kr, qq, lo, qo, T, 16]), f"flat {-(-T // 4)} x 256",
+        "non-temporal, one wave per token, q in batches of 8 vectors per lane")
+    row("k3h_mla_rope_pack (the operator, cfg 4)", "RoPE pack", rope_bytes,
+        lambda: ctx.mla_rope_pack(lat, kr, qq, gk, pos, lo, qo, T, 16, stream=s), "typed call", "non-temporal")
+    del lat, kr, qq, lo, qo
     # residual push v3 at nb 0, 4 ranks (the per-op table's (f)1 row): one row
     # read, the snapshot slot and four normed copies written
     B = T // 4

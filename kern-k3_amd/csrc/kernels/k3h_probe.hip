@@ -36,6 +36,10 @@
 //   k3h_probe_rowgather(src, idx, dst, R, cols)   the MXFP8 permute's payload:
 //       dst[r] = src[idx[r]] (cols bytes, cols % 1024 == 0), one wave per row,
 //       4 rows per 256-thread workgroup, all of a row's loads before its stores.
+//   k3h_probe_rope(latent, k_rope, q, latent_out, q_out, T, H)   the MLA latent
+//       norm + RoPE + q pack: one wave per token moves its latent and k_rope
+//       rows and its H x 192 q values, as the operator's loads and stores do
+//       (H must be 16; any other H stores nothing).
 //   k3h_probe_push_t<NT>(src, snap, n0, n1, n2, n3, B)   the nb-0 residual push
 //       at 4 ranks: one row read, five written (the snapshot slot and four
 //       normed copies), grid B, NT = 128 (7 vectors per lane) or 896 (1).
@@ -290,6 +294,42 @@ K3_DEV void kp_push(const k3_u4* __restrict__ src, k3_u4* __restrict__ snap, k3_
   }
 KP_PUSH(128)
 KP_PUSH(896)
+
+// The MLA latent norm + RoPE + q pack: one wave per token (4 tokens per
+// 256-thread workgroup) moves the token's latent row (1 KB, one vector per lane)
+// and k_rope (128 B, lanes 0-7) to latent_out (1152 B) and its H x 192 q values
+// (H * 24 vectors, in batches of 8 per lane) to q_out, every load of a token
+// before its first store; the RoPE and the norm replaced by moves.
+extern "C" __global__ void __launch_bounds__(256) k3h_probe_rope(
+    const k3_u4* __restrict__ latent, const k3_u4* __restrict__ k_rope, const k3_u4* __restrict__ q,
+    k3_u4* __restrict__ latent_out, k3_u4* __restrict__ q_out, int T, int H) {
+  const int l = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T || H != 16) return;
+  // H fixed at 16 (the config's heads): with a run-time count the compiler
+  // guards each q load with a branch and a full wait, which serialises them
+  constexpr int nvec = 16 * 24;
+  const k3_u4 x = __builtin_nontemporal_load(latent + (size_t)t * 64 + l);
+  k3_u4 kr = {0u, 0u, 0u, 0u};
+  if (l < 8) kr = k_rope[(size_t)t * 8 + l];
+  const k3_u4* qrow = q + (size_t)t * nvec;
+  k3_u4* orow = q_out + (size_t)t * nvec;
+  k3_u4 a[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    if (64 * k < nvec) a[k] = __builtin_nontemporal_load(qrow + min(l + 64 * k, nvec - 1));
+  __builtin_nontemporal_store(x, latent_out + (size_t)t * 72 + l);
+  if (l < 8) __builtin_nontemporal_store(kr, latent_out + (size_t)t * 72 + 64 + l);
+  for (int w0 = 0; w0 < nvec; w0 += 64 * 8) {
+    if (w0 > 0) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (w0 + 64 * k < nvec) a[k] = __builtin_nontemporal_load(qrow + min(w0 + l + 64 * k, nvec - 1));
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (w0 + l + 64 * k < nvec) __builtin_nontemporal_store(a[k], orow + w0 + l + 64 * k);
+  }
+}
 
 // ---------------------------------------------------------------- MFMA rate
 template <int FA, int FB>
