@@ -64,6 +64,7 @@ class Ranks:
 @pytest.mark.parametrize("nb,snapshot,B,rank,nranks", [
     (0, 1, 37, 1, 4),     # the manifest's first-layer call (nb 0, snapshot 1): the 896-thread entry
     (0, 0, 5, 0, 1),      # nb 0, one rank, no snapshot
+    (0, 1, 19, 7, 8),     # nb 0, eight ranks (the most), last rank
     (3, 0, 16, 0, 4),
     (8, 1, 9, 3, 4),      # nb = 8: no snapshot slot left
     (2, 1, 5, 0, 1),      # one rank: no peers read

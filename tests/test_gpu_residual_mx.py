@@ -74,15 +74,18 @@ def test_k1b_mixing(ctx, land, nb, snapshot):
 
 
 @pytest.mark.parametrize("nb", range(1, 9))
-def test_k1b_per_nb_entries(ctx, nb):
+@pytest.mark.parametrize("snapshot", [0, 1])
+def test_k1b_per_nb_entries(ctx, nb, snapshot):
+    """The typed nb entries (vector-split body) against the oracle; with snapshot
+    the prefix row is not read and prefix2 is the landed partial."""
     B = 12
-    _case(f"k1b_nb{nb}")
+    _case(f"k1b_nb{nb} snapshot={snapshot}")
     prefix, partial, blocks, sw, gamma = _k1_inputs(300 + nb, B)
-    want_p2, want_n = O.land_add_attnres_rms(partial, prefix, blocks, sw, gamma, nb, 0, B)
+    want_p2, want_n = O.land_add_attnres_rms(partial, prefix, blocks, sw, gamma, nb, snapshot, B)
     p2 = torch.empty((B, H), dtype=torch.bfloat16, device="cuda")
     nrm = torch.empty_like(p2)
     ctx.land_add_attnres_rms_nb(to_dev(partial), to_dev(prefix), to_dev(blocks), to_dev(sw),
-                                to_dev(gamma), p2, nrm, nb, 0, B)
+                                to_dev(gamma), p2, nrm, nb, snapshot, B)
     torch.cuda.synchronize()
     _eq("prefix2", from_dev(p2), want_p2)
     _eq("normed", from_dev(nrm), want_n)
