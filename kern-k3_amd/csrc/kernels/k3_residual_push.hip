@@ -18,7 +18,8 @@
 // Typed-call entries k3h_attnres_rms_push_nb{K}s (K = 1..8, nb == K; same
 // parameter list as the module's entry, block 256): the vector-split row body
 // (k3_residual_split.h), every candidate held on chip from pass 1 to pass 2,
-// the same bits.
+// the same bits; and k3h_attnres_rms_push_nb0w896 (nb == 0, block 896: one
+// vector of the row per lane, below), the same bits as the nb-0 branch.
 //
 // Row b of this rank lands at row rank * B + b of every rank's normed_all: the
 // local copy through `normed_all`, the others through dst_peer[q] (q < nranks,
