@@ -766,6 +766,16 @@ def bench_push_land(ctx, add, timed, bf, g, s, O=None, h=None) -> None:
         f"B={B} nb={nb} two=1", 3 * row + nb * row + 2 * HH * 4 + HH * 2 + row + row + 4 * row + B * nb * 8,
         timed(lambda: ctx.attnres_rms_push_add2(blocks, sw, gm, normed[0], peer, nb, 1, B, 0, 4,
                                                 sw_mlp, stats, p1, p2, prefix2, hidden, 1, stream=s)))
+    # normed_sync: the arrival barrier after the push, every peer already arrived
+    # (their slot counters at the top of the 32-bit range, so every call passes)
+    flags = [torch.zeros(372, dtype=torch.int64, device="cuda") for _ in range(4)]
+    for q in (0, 2, 3):
+        flags[q][1] = 0xFFFFFFFF
+    fpeer = torch.tensor([f.data_ptr() for f in flags], dtype=torch.int64, device="cuda")
+    ctx.epoch_bump(flags[1], 896, stream=s)
+    add("arrival barrier (normed_sync, peers arrived)", "kern_k3_rs_arrive1", "1 wave, 4 ranks", 0,
+        timed(lambda: ctx.rs_arrive(flags[1], fpeer, 896, 1, 4, stream=s)),
+        "fence, add, 4 polls, fence")
     part = bf(B, HH)
     pre2, nrm = torch.empty_like(part), torch.empty_like(part)
     for k, kern in ((1, "k3h_land_add_attnres_rms_nb1s"), (4, "k3h_land_add_attnres_rms_nb4s"),
@@ -886,6 +896,7 @@ OP_KERNELS = {
     "weighted finalize (cfg 5d)": ["k3h_moe_finalize_rows"],
     "residual push v3 (res_in, nb 0, 4 ranks)": ["k3h_attnres_rms_push_nb0w896"],
     "residual push_add2 (res_in, nb 4, 4 ranks)": ["k3h_attnres_rms_push_nb4s"],
+    "arrival barrier (normed_sync, peers arrived)": ["kern_k3_rs_arrive1"],
     "K1b nb 1 (res_mlp, typed call)": ["k3h_land_add_attnres_rms_nb1s"],
     "K1b nb 4 (res_mlp, typed call)": ["k3h_land_add_attnres_rms_nb4s"],
     "K1b nb 8 (res_mlp, typed call)": ["k3h_land_add_attnres_rms_nb8s"],

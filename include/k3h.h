@@ -135,6 +135,31 @@ K3H_API int k3h_land_add_attnres_rms_nb_stats(k3h_ctx_t ctx, void* stream, const
 K3H_API int k3h_land_add2_bf16(k3h_ctx_t ctx, void* stream, const void* p1, const void* p2,
                                const void* prefix2, void* hidden, int two, int B);
 
+/* ---- epoch / arrival barrier of the push family ------------------------------
+ * flags: this rank's u64 counters (the manifest's coll_flags [372]); flags[0] is
+ * the epoch.  flags_peer: u64 device addresses of every rank's flags, rank q at
+ * [q] (the manifest's coll_flags_peer).  Counters are never reset after init.
+ * kern_k3_flags_init (k3_collectives.cu:64; op k3_flags_init of the load program,
+ * k3-tp4-prefill-16k.json:406338): flags[0 .. n) = 0.  Grid 1, block 256. */
+K3H_API int k3h_flags_init(k3h_ctx_t ctx, void* stream, unsigned long long* flags, int n);
+/* kern_k3_epoch_bump (k3_collectives.cu:74; op k3_epoch_bump, the first call of
+ * every prefill, json:406299): flags[0] += units, the arrivals the call's
+ * collectives will add per slot (the collective grid: 896 at 16,384 tokens).
+ * Grid (units), block 64: the entry adds its grid size. */
+K3H_API int k3h_epoch_bump(k3h_ctx_t ctx, void* stream, unsigned long long* flags, int units);
+/* kern_k3_rs_arrive1 (k3_rs_arrive_v2.cu:41; module k3_rs_arrive_v2 of op
+ * k3_allgather_push, json:406354, the normed_sync after every residual push, and
+ * the first launch of k3_reducescatter_bf16, json:406431): flags[slot] += units,
+ * then wait until every rank q < nranks has flags_peer[q][slot] >= flags[0]
+ * (low 32 bits compared), giving up after 2 s per rank.  1 <= slot, 1 <= nranks
+ * <= 8.  Grid 1, block 64.  missing == NULL launches the manifest entry; else the
+ * entry k3h_rs_arrive_mask (no counterpart in the reference) runs the same
+ * barrier and writes *missing (device u32) = mask of the ranks that had not
+ * arrived when the wait gave up, 0 when all did. */
+K3H_API int k3h_rs_arrive(k3h_ctx_t ctx, void* stream, unsigned long long* flags,
+                          const unsigned long long* flags_peer, int units, int slot, int nranks,
+                          unsigned* missing);
+
 /* ---- landing kernels (shared-expert MLP, MoE latent norm) -------------------
  * The entries run under the manifests' grids; these typed calls launch compact
  * grids of 256-thread blocks sized to the work where the shape allows (the

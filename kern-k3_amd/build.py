@@ -54,6 +54,9 @@ SOURCES = {
     "k3_land_fused": "k3_land.hip",
     "k3h_moe_gemm": "k3h_moe_gemm.hip",
     "k3h_probe": "k3h_probe.hip",
+    "k3_collectives": "k3_barrier.hip",
+    "k3_rs_arrive1": "k3_barrier.hip",
+    "k3_rs_arrive_v2": "k3_barrier.hip",
 }
 
 # defines implied by a base name that shares its source with another base
@@ -103,6 +106,10 @@ MODULES = [
     "k3_land_fused",
     "k3h_moe_gemm",
     "k3h_probe",
+    "k3_collectives",
+    "k3_rs_arrive1",
+    "k3_rs_arrive_v2",
+    "k3_rs_arrive_v2+K3_SPIN_US=20000",  # 20 ms give-up: the missing-rank tests
 ]
 
 DEVICE_FLAGS = [

@@ -148,4 +148,40 @@ K3H_API int k3h_land_add2_bf16(k3h_ctx_t ctx, void* stream, const void* p1, cons
                  stream, a);
 }
 
+// ---- epoch / arrival barrier (module k3_barrier.hip) -----------------------
+
+K3H_API int k3h_flags_init(k3h_ctx_t ctx, void* stream, unsigned long long* flags, int n) {
+  if (!ctx || n < 0 || !k3h_okp(flags, 8)) return K3H_EINVAL;
+  if (n == 0) return K3H_OK;
+  K3hArgs a;
+  a.ptr(flags).i32(n);
+  return k3h_run(ctx, "k3_collectives", "kern_k3_flags_init", 1, 1, 1, 256, stream, a);
+}
+
+// kern_k3_epoch_bump adds its grid size; one 64-thread workgroup per unit (the
+// reference's 1024-thread workgroups add the same count).
+K3H_API int k3h_epoch_bump(k3h_ctx_t ctx, void* stream, unsigned long long* flags, int units) {
+  if (!ctx || units < 1 || !k3h_okp(flags, 8)) return K3H_EINVAL;
+  K3hArgs a;
+  a.ptr(flags);
+  return k3h_run(ctx, "k3_collectives", "kern_k3_epoch_bump", (uint32_t)units, 1, 1, 64, stream,
+                 a);
+}
+
+K3H_API int k3h_rs_arrive(k3h_ctx_t ctx, void* stream, unsigned long long* flags,
+                          const unsigned long long* flags_peer, int units, int slot, int nranks,
+                          unsigned* missing) {
+  if (!ctx || units < 1 || slot < 1 || nranks < 1 || nranks > kMaxRanks) return K3H_EINVAL;
+  if (!k3h_okp(flags, 8) || !k3h_okp(flags_peer, 8)) return K3H_EINVAL;
+  if (missing && !k3h_okp(missing, 4)) return K3H_EINVAL;
+  K3hArgs a;
+  if (!missing) {  // the manifest entry (src, dst, src_peer, count, order, rank unused)
+    a.ptr(nullptr).ptr(nullptr).ptr(nullptr).ptr(flags).ptr(flags_peer).i64(0);
+    a.i32(units).i32(slot).i32(6).i32(0).i32(nranks);
+    return k3h_run(ctx, "k3_rs_arrive_v2", "kern_k3_rs_arrive1", 1, 1, 1, 64, stream, a);
+  }
+  a.ptr(flags).ptr(flags_peer).i32(units).i32(slot).i32(nranks).ptr(missing);
+  return k3h_run(ctx, "k3_rs_arrive_v2", "k3h_rs_arrive_mask", 1, 1, 1, 64, stream, a);
+}
+
 }  // extern "C"

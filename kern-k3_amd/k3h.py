@@ -93,6 +93,9 @@ _SIGS: dict[str, list] = {
                                   _P, _P, _I],
     "k3h_land_add_attnres_rms_nb_stats": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _I],
     "k3h_land_add2_bf16": [_P, _P, _P, _P, _P, _P, _I, _I],
+    "k3h_flags_init": [_P, _P, _P, _I],
+    "k3h_epoch_bump": [_P, _P, _P, _I],
+    "k3h_rs_arrive": [_P, _P, _P, _P, _I, _I, _I, _P],
     "k3h_rms": [_P, _P, _P, _P, _P, _I, _I],
     "k3h_land": [_P, _P, _P, _P, _I, _I, _I, _I],
     "k3h_land_situ": [_P, _P, _I, _P, _P, _I, _I],
@@ -358,6 +361,30 @@ class Ctx:
         _dev(hidden, "hidden", BF16, B * H)
         _check(self.L.k3h_land_add2_bf16(self.h, _stream(stream), _ptr(p1), _ptr(p2),
                                          _ptr(prefix2), _ptr(hidden), two, B), "land_add2_bf16")
+
+    # ------------------------------------------------------------ epoch / arrival barrier
+    def flags_init(self, flags, n: int, stream=None) -> None:
+        """kern_k3_flags_init (k3_collectives.cu:64): flags[0 .. n) = 0."""
+        _dev(flags, "flags", I64, n, align=8)
+        _check(self.L.k3h_flags_init(self.h, _stream(stream), _ptr(flags), n), "flags_init")
+
+    def epoch_bump(self, flags, units: int, stream=None) -> None:
+        """kern_k3_epoch_bump (k3_collectives.cu:74): flags[0] += units."""
+        _dev(flags, "flags", I64, 1, align=8)
+        _check(self.L.k3h_epoch_bump(self.h, _stream(stream), _ptr(flags), units), "epoch_bump")
+
+    def rs_arrive(self, flags, flags_peer, units: int, slot: int, nranks: int, missing=None,
+                  stream=None) -> None:
+        """kern_k3_rs_arrive1 (k3_rs_arrive_v2.cu:41): flags[slot] += units, then wait until
+        every rank's flags[slot] (flags_peer: int64 tensor of device addresses) reaches
+        flags[0].  With ``missing`` (int32 [1]) the mask of ranks that never arrived is
+        written there."""
+        _dev(flags, "flags", I64, slot + 1, align=8)
+        _dev(flags_peer, "flags_peer", I64, nranks, align=8)
+        if missing is not None:
+            _dev(missing, "missing", I32, 1, align=4)
+        _check(self.L.k3h_rs_arrive(self.h, _stream(stream), _ptr(flags), _ptr(flags_peer), units,
+                                    slot, nranks, _ptr(missing)), "rs_arrive")
 
     # ------------------------------------------------------------ landing kernels
     def rms(self, x, gamma, o, h: int, B: int, stream=None) -> None:

@@ -141,6 +141,12 @@ void k3o_moe_gemm_mx_abs(const uint8_t* a, const uint8_t* a_sf, const int* a_row
                          const int* cta_batch, int E, int N, int K, double* out);
 void k3o_situ_ab_n(const float* g, const float* u, float* y, size_t n, float alpha, float beta);
 
+/* ---- epoch / arrival barrier for host threads (k3_oracle_barrier.c) */
+void k3o_flags_init(uint64_t* flags, int n);
+void k3o_epoch_bump(uint64_t* flags, int units);
+unsigned k3o_rs_arrive(uint64_t* flags, const uint64_t* flags_peer, int units, int slot,
+                       int nranks, long long spin_ns);
+
 #ifdef __cplusplus
 }
 #endif

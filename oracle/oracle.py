@@ -47,6 +47,11 @@ def lib() -> ctypes.CDLL:
         _lib.k3o_situ.argtypes = [ctypes.c_float, ctypes.c_float]
         _lib.k3o_e2m1_decode.restype = ctypes.c_float
         _lib.k3o_e2m1_decode.argtypes = [ctypes.c_uint8]
+        _lib.k3o_rs_arrive.restype = ctypes.c_uint
+        _lib.k3o_rs_arrive.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                       ctypes.c_int, ctypes.c_int, ctypes.c_longlong]
+        _lib.k3o_epoch_bump.argtypes = [ctypes.c_void_p, ctypes.c_int]
+        _lib.k3o_flags_init.argtypes = [ctypes.c_void_p, ctypes.c_int]
     return _lib
 
 
@@ -435,3 +440,26 @@ def moe_fc1_epilogue(c, alpha_rows, beta_rows):
             x[r] = situ_ab(g[r], u[r], float(alpha_rows[r]), float(beta_rows[r]))
     x16 = bf(x)
     return moe_quant(x16, rows, half)
+
+
+# ---- epoch / arrival barrier (host threads play the ranks)
+def flags_init(flags: np.ndarray) -> None:
+    """kern_k3_flags_init: every counter of a uint64 array to 0."""
+    assert flags.dtype == np.uint64
+    lib().k3o_flags_init(_p(flags), flags.size)
+
+
+def epoch_bump(flags: np.ndarray, units: int) -> None:
+    """kern_k3_epoch_bump: flags[0] += units."""
+    lib().k3o_epoch_bump(_p(flags), units)
+
+
+def rs_arrive(flags: np.ndarray, flags_peer: np.ndarray, units: int, slot: int, nranks: int,
+              spin_ns: int) -> int:
+    """kern_k3_rs_arrive1: flags[slot] += units, then wait (at most spin_ns) until every
+    rank's counter (flags_peer: uint64 addresses) reaches flags[0]; returns the mask of
+    the ranks given up on.  The GIL is released for the call (ctypes), so threads can
+    play the ranks."""
+    assert flags.dtype == np.uint64 and flags_peer.dtype == np.uint64
+    return int(lib().k3o_rs_arrive(_p(flags), _p(flags_peer), units, slot, nranks, spin_ns))
+

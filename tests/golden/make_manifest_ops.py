@@ -18,6 +18,8 @@ HOT = {
         # residual push family and landing kernels
         "attnres_rms_push_first_v3", "attnres_rms_push_add2", "land_add_attnres_rms_bf16_v2_nb4",
         "land_add_attnres_rms_bf16_v2_nb8", "land_situ_n33792", "land_situ_rms",
+        # epoch / arrival barrier (normed_sync after the push; coll_epoch; the load program's init)
+        "k3_allgather_push", "k3_epoch_bump", "k3_flags_init",
     ],
     "k3-tp4-prefill-16k-l0-bf16.json": [
         "attnres_rms_v2", "land_add_attnres_rms_bf16_v2", "land_add2_v2",

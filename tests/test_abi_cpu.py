@@ -74,6 +74,15 @@ def test_host_validation_rejects_before_launch(hctx):
     assert L.k3h_moe_quant(h, None, A, A, A, 3, 7) == E  # 21 elements: not whole blocks
     assert L.k3h_attnres_rms(h, None, A + 1, A, A, A, A, 0, 0, 1, 1e-5) == E
     assert L.k3h_land_add2(h, None, A, None, A, A, 1, 1) == E
+    # barrier: slot 0 is the epoch, 1 <= nranks <= 8, units >= 1, 8-byte counters
+    assert L.k3h_rs_arrive(h, None, A, A, 896, 0, 4, None) == E
+    assert L.k3h_rs_arrive(h, None, A, A, 896, 1, 9, None) == E
+    assert L.k3h_rs_arrive(h, None, A, A, 0, 1, 4, None) == E
+    assert L.k3h_rs_arrive(h, None, A + 4, A, 896, 1, 4, None) == E
+    assert L.k3h_rs_arrive(h, None, A, None, 896, 1, 4, None) == E
+    assert L.k3h_rs_arrive(h, None, A, A, 896, 1, 4, A + 2) == E
+    assert L.k3h_epoch_bump(h, None, A, 0) == E
+    assert L.k3h_flags_init(h, None, A + 4, 372) == E
 
 
 def test_empty_work_returns_ok_without_launch(hctx):
@@ -82,6 +91,7 @@ def test_empty_work_returns_ok_without_launch(hctx):
     assert L.k3h_moe_quant(h, None, A, A, A, 0, 7168) == 0
     assert L.k3h_land_add_attnres_rms(h, None, 1, A, A, None, None, A, A, A, 0, 0, 0, 1e-5) == 0
     assert L.k3h_land_add2(h, None, A, None, A, A, 0, 0) == 0
+    assert L.k3h_flags_init(h, None, A, 0) == 0
 
 
 def test_launch_rejects_bad_block():
