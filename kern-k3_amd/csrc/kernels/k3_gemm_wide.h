@@ -404,9 +404,22 @@ K3_DEV void k3w_gemm_bf16(K3G_PARAMS, uint16_t* __restrict__ out) {
         k3g_swap(d[1], d[5]);
         k3g_swap(d[2], d[6]);
         k3g_swap(d[3], d[7]);
-        uint16_t* o = out + K3W_LANE_ROW(mt) * N + K3W_TILE_COL(nt) + 16 * h;
-        k3_st16(o, (k3_u4){d[0], d[1], d[4], d[5]});
-        k3_st16(o + 8, (k3_u4){d[2], d[3], d[6], d[7]});
+        // Lane (j, h) now holds 16-byte chunks 2 h (X) and 2 h + 1 (Y) of row j's 64
+        // bytes.  Lanes j and j ^ 1 (DPP quad_perm [1,0,3,2]) trade one chunk, the
+        // even lane its Y, the odd lane its X, so that each store writes 16 rows x 64
+        // contiguous bytes (the even rows, then the odd ones) instead of 32 rows x
+        // two 16-byte pieces: half the write requests (measured: fc2 4% faster).
+        const int p = threadIdx.x & 1;
+        const k3_u4 X = {d[0], d[1], d[4], d[5]}, Y = {d[2], d[3], d[6], d[7]};
+        const k3_u4 snd = p ? X : Y;
+        k3_u4 rcv;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          rcv[c] = (uint32_t)__builtin_amdgcn_mov_dpp((int)snd[c], K3_DPP_QP_1032, 0xf, 0xf, false);
+        uint16_t* o = out + (K3W_LANE_ROW(mt) & ~(size_t)1) * N + K3W_TILE_COL(nt) + 8 * (2 * h + p);
+        k3_st16(o, p ? rcv : X);      // row j & ~1: chunk 2 h + p
+        k3_st16(o + N, p ? Y : rcv);  // row j | 1
+
       }
   });
 }
