@@ -982,6 +982,8 @@ def traffic_table(fetch_csv: str, write_csv: str, ops_json: str) -> str:
         rd = sum(f) * 1024 * kf
         wr = sum(w) * 1024 * kw
         alg = ops[op]["bytes"]
+        if not alg:  # latency rows (the arrival barrier) move no payload
+            continue
         out.append(f"| {op} | {', '.join('`%s`' % k for k in kernels)} | {rd:,.0f} | {wr:,.0f} | "
                    f"{rd + wr:,.0f} | {alg:,} | {(rd + wr) / alg:.3f} |")
     return "\n".join(out)
@@ -1024,6 +1026,8 @@ def trace_table(trace_csv: str, ops_json: str) -> str:
         us = clean[len(clean) // 2]
         if r.get("bound") == "mfma":
             rate = f" | | | {r['flops'] / (us * 1e-6) / 1e12:.1f}"
+        elif not r["bytes"]:  # latency rows (the arrival barrier) move no payload
+            rate = " | | | "
         else:
             gbs = r["bytes"] / (us * 1e-6) / 1e9
             rate = f" | {gbs:.1f} | {100 * gbs / PEAK_GBS:.1f} | "

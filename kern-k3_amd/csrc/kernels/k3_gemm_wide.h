@@ -419,7 +419,6 @@ K3_DEV void k3w_gemm_bf16(K3G_PARAMS, uint16_t* __restrict__ out) {
         uint16_t* o = out + (K3W_LANE_ROW(mt) & ~(size_t)1) * N + K3W_TILE_COL(nt) + 8 * (2 * h + p);
         k3_st16(o, p ? rcv : X);      // row j & ~1: chunk 2 h + p
         k3_st16(o + N, p ? Y : rcv);  // row j | 1
-
       }
   });
 }
