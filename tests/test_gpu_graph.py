@@ -9,7 +9,9 @@ run eagerly into a second set of outputs, and every output of the replay must
 equal the eager one bit for bit.  Outputs are refilled with a sentinel (a torch
 fill kernel, outside the graph) before every replay and eager run, so a launch
 that the graph dropped shows up as sentinel bytes.  The library issues no
-memset or allocation, so nothing but kernel nodes is recorded."""
+memset or allocation, so nothing but kernel nodes is recorded.  A second graph
+holds the arrival barrier that follows the push (epoch bump, a peer's arrival
+played by a torch add, the one-wave wait), replayed between eager runs."""
 import numpy as np
 import pytest
 import torch
@@ -175,4 +177,46 @@ def test_graph_replays_match_eager(ctx):
         # the push reached both buffers and the routing produced rows
         assert int(e_out["tp"][0]) > 0
         assert torch.equal(_bits(e_out["normed_all"][T:]), _bits(e_out["peer_all"][T:]))
+    graph.reset()
+
+
+def test_graph_replays_the_arrival_barrier(ctx):
+    """The res_in sequence's barrier part captured: the epoch bump, the peer's
+    arrival (played by a torch add on its counter, a kernel node) and the one-wave
+    arrival wait.  Replays and eager runs alternate; every one must leave the
+    counters at the protocol's totals and report no rank given up on (a wait that
+    gave up would also take 2 s)."""
+    _case("graph capture of epoch bump + peer arrival + arrive")
+    own = torch.zeros(372, dtype=torch.int64, device="cuda")
+    peer = torch.zeros(372, dtype=torch.int64, device="cuda")
+    fpeer = torch.tensor([own.data_ptr(), peer.data_ptr()], dtype=torch.int64, device="cuda")
+    missing = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    units, slot = 896, 3
+
+    def seq():
+        ctx.epoch_bump(own, units)
+        peer[slot] += units
+        ctx.rs_arrive(own, fpeer, units, slot, 2, missing)
+
+    seq()  # loads the code objects before capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        seq()
+    torch.cuda.synchronize()
+    calls = 1
+    for r in range(4):
+        _case(f"barrier replay {r}")
+        missing.fill_(-1)
+        graph.replay()
+        calls += 1
+        torch.cuda.synchronize()
+        assert int(missing[0]) == 0, f"replay {r}: ranks given up on {int(missing[0])}"
+        missing.fill_(-1)
+        seq()  # eager between replays
+        calls += 1
+        torch.cuda.synchronize()
+        assert int(missing[0]) == 0
+        total = calls * units
+        assert int(own[0]) == total and int(own[slot]) == total and int(peer[slot]) == total
     graph.reset()
