@@ -209,3 +209,23 @@ def test_manifest_push_then_normed_sync(ctx):
     for q in range(4):
         got = from_dev(normed[q])[rank * B:(rank + 1) * B]
         assert (got == wn).all(), f"normed_all[{q}]"
+
+
+def test_arrive_compares_the_low_word(ctx):
+    """As the reference (k3_rs_arrive1.cu:56-58) and the oracle: the wait compares
+    the low 32 bits, so a peer counter past 2^32 compares by its low word."""
+    _case("low-word comparison")
+    own = torch.zeros(SLOTS, dtype=torch.int64, device="cuda")
+    peer = torch.zeros(SLOTS, dtype=torch.int64, device="cuda")
+    fpeer = torch.tensor([own.data_ptr(), peer.data_ptr()], dtype=torch.int64, device="cuda")
+    missing = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    arrive = _op(ctx, SHORT, "k3h_rs_arrive_mask", MASK_SPEC)
+    own[0] = (1 << 32) + 5   # epoch: low word 5
+    peer[4] = 7              # low word 7 >= 5 (the u64 far below the epoch)
+    arrive([own, fpeer, 5, 4, 2, missing], {})
+    torch.cuda.synchronize()
+    assert int(missing[0]) == 0
+    peer[5] = (1 << 32) + 3  # low word 3 < 5 (the u64 above 5): given up on after 20 ms
+    arrive([own, fpeer, 5, 5, 2, missing], {})
+    torch.cuda.synchronize()
+    assert int(missing[0]) == 0b10

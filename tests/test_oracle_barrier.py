@@ -146,3 +146,14 @@ def test_single_rank_passes_on_its_own_arrival():
     O.epoch_bump(R.flags[0], 896)
     assert O.rs_arrive(R.flags[0], R.peer, 896, 7, 1, 1000) == 0
     assert int(R.flags[0][7]) == 896
+
+
+def test_comparison_is_on_the_low_word():
+    """The wait compares the low 32 bits of the counters (k3_rs_arrive1.cu:56-58):
+    a counter past 2^32 compares by its low word."""
+    R = Ranks(2)
+    R.flags[0][0] = (1 << 32) + 5          # epoch: low word 5
+    R.flags[1][4] = 7                       # peer: low word 7 >= 5, the u64 far below the epoch
+    assert O.rs_arrive(R.flags[0], R.peer, 5, 4, 2, 1_000_000) == 0  # own counter 5
+    R.flags[1][5] = (1 << 32) + 3           # peer: low word 3 < 5, the u64 above 5
+    assert O.rs_arrive(R.flags[0], R.peer, 5, 5, 2, 1_000_000) == 0b10
