@@ -191,3 +191,72 @@ def test_manifest_kda_ops(ctx):
     torch.cuda.synchronize()
     want = O.kda_out_gate(attn, sp.partial, gamma_o, np.zeros((tokens, INNER), np.uint16), 0, tokens)
     _close1("gated", from_dev(gated), want)
+
+
+def _special_match(name, got, want):
+    """NaN positions and infinities (with sign) identical; finite values within one ulp."""
+    gf, wf = bf16_to_f32(np.asarray(got)), bf16_to_f32(np.asarray(want))
+    gn, wn = np.isnan(gf), np.isnan(wf)
+    assert np.array_equal(gn, wn), f"{name}: NaN positions differ ({gn.sum()} vs {wn.sum()})"
+    gi, wi = np.isinf(gf), np.isinf(wf)
+    assert np.array_equal(gi, wi) and np.array_equal(np.sign(gf[gi]), np.sign(wf[wi])), \
+        f"{name}: infinities differ"
+    fin = ~(gn | gi)
+    d = ulp_diff_bf16(np.asarray(got)[fin], np.asarray(want)[fin])
+    print(f"  {name}: {gn.sum()} NaN, {gi.sum()} inf, finite max ulp {d.max() if d.size else 0}",
+          flush=True)
+    assert d.size == 0 or d.max() <= 1, name
+
+
+SPECIALS = np.array([0x7FC0, 0xFFC1, 0x7F80, 0xFF80, 0x7F7F, 0xFF7F, 0x0001, 0x8000], np.uint16)
+
+
+def test_span_gather_special_values(ctx):
+    """NaN (either sign), +-inf, +-max finite, a subnormal and -0 in the q/k/v bands
+    and in the carried window: the conv and SiLU propagate them as the oracle does
+    (SiLU(-inf) and inf - inf give NaN, SiLU(+inf) = +inf), within one ulp elsewhere;
+    the landing copies and the window stay bit-exact."""
+    _case("span_gather special values")
+    sp = Span(40, 2500)
+    g = rng(2501)
+    flat = sp.partial.reshape(-1)
+    pos = g.choice(flat.size, 64, replace=False)
+    flat[pos] = SPECIALS[np.arange(64) % SPECIALS.size]
+    w = sp.win.reshape(-1)
+    wpos = g.choice(w.size, 16, replace=False)
+    w[wpos] = SPECIALS[np.arange(16) % SPECIALS.size]
+    off = sp.line * LINE_BYTES + REC_BYTES
+    sp.state0[off:off + 3 * WIN_BYTES] = sp.win.reshape(-1).view(np.uint8)
+    sp.d_state = to_dev(sp.state0)
+    sp.d_partial = to_dev(sp.partial)
+    q, k, v, beta, flow, nw = O.span_gather(sp.partial, sp.cw, sp.win, sp.wsm, 2, 33)
+    got = sp.run(ctx, 2, 33)
+    for nm, gq, wq in zip("qkv", got[:3], (q, k, v)):
+        _special_match(f"span_{nm}", gq, wq)
+    assert np.array_equal(got[3], beta) and np.array_equal(got[4], flow)
+    win, _ = sp.window()
+    assert np.array_equal(win, nw)
+
+
+def test_kda_out_gate_special_values(ctx):
+    """NaN and +-inf in attention rows (a NaN or an infinity makes its head's
+    sum of squares NaN / inf, so r is NaN / 0) and in the gate (sigmoid(+-inf) =
+    1 / 0, NaN stays NaN): positions and values as the oracle's."""
+    _case("kda_out_gate special values")
+    rows, at, span = 40, 3, 30
+    g = rng(2600)
+    attn = normal_bf16(g, (span, INNER))
+    gate = normal_bf16(g, (rows, 4 * INNER))
+    a = attn.reshape(-1)
+    a[g.choice(a.size, 24, replace=False)] = SPECIALS[np.arange(24) % SPECIALS.size]
+    gb = gate[:, 3 * INNER:].copy().reshape(-1)
+    gb[g.choice(gb.size, 24, replace=False)] = SPECIALS[np.arange(24) % SPECIALS.size]
+    gate[:, 3 * INNER:] = gb.reshape(rows, INNER)
+    gamma_o = (1.0 + 0.1 * g.standard_normal(128)).astype(np.float32)
+    want = O.kda_out_gate(attn, gate, gamma_o, np.zeros((rows, INNER), np.uint16), at, span, eps=1e-6)
+    gated = torch.zeros((rows, INNER), dtype=torch.bfloat16, device="cuda")
+    ctx.kda_out_gate(to_dev(attn), to_dev(gate), to_dev(gamma_o), gated,
+                     to_dev(np.array([at], np.int32)), span, eps=1e-6)
+    torch.cuda.synchronize()
+    got = from_dev(gated)
+    _special_match("gated", got[at:at + span], want[at:at + span])

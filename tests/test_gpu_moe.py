@@ -438,3 +438,41 @@ def test_manifest_router_and_routing_ops(ctx):
         [to_dev(fc2), e2p, to_dev(w16), out, tokens], env)
     torch.cuda.synchronize()
     _eq("finalize", from_dev(out), O.moe_finalize(fc2, we, w16, tokens, 16, 3584))
+
+
+def test_finalize_special_values(ctx):
+    """NaN (either sign), +-inf, +-max finite, a subnormal and -0 in the expert
+    output rows and NaN / +-inf in the routing weights: each token's weighted sum
+    carries them as the oracle's fixed-order sum (inf - inf and 0 x inf give NaN,
+    sums past the largest finite round to inf); both the typed call and the
+    manifest entry."""
+    specials = np.array([0x7FC0, 0xFFC1, 0x7F80, 0xFF80, 0x7F7F, 0xFF7F, 0x0001, 0x8000], np.uint16)
+    topk, cols = 8, 1032
+    _case("finalize special values")
+    g = rng(1790)
+    T, rows = 60, 97
+    e2p = np.full((T, topk), -1, dtype=np.int32)
+    for t in range(T):
+        live = g.choice(topk, size=t % (topk + 1), replace=False)
+        e2p[t, live] = g.integers(0, rows, size=live.size)
+    wts = g.random((T, topk), dtype=np.float32) * 2 - 0.5
+    wts.reshape(-1)[g.choice(T * topk, 6, replace=False)] = [np.nan, np.inf, -np.inf, 0.0, 3e38, -0.0]
+    fc2 = normal_bf16(g, (rows, cols))
+    flat = fc2.reshape(-1)
+    flat[g.choice(flat.size, 200, replace=False)] = specials[np.arange(200) % specials.size]
+    want = O.moe_finalize(fc2, e2p.reshape(-1), wts, T, topk, cols)
+    d_fc2, d_e2p, d_wts = to_dev(fc2), to_dev(e2p.reshape(-1)), to_dev(wts)
+    out = torch.empty((T, cols), dtype=torch.bfloat16, device="cuda")
+    ctx.moe_finalize(d_fc2, d_e2p, d_wts, out, T, cols, topk=topk)
+    spec = {"params": ["in buffer<bf16>", "in buffer<i32>", "in buffer<f32>", "out buffer<bf16>",
+                       "i32", "i32"],
+            "impl": {"launches": [{"module": _MOE_V4 + "+TOPK=8", "entry": "kern_k3_moe_finalize",
+                                   "grid": [{"ceil_div": ["tokens", 2]}, 1, 1], "block": [128, 1, 1]}]}}
+    out2 = torch.empty((T, cols), dtype=torch.bfloat16, device="cuda")
+    k3h.ManifestOp(ctx, "moe_finalize", spec)([d_fc2, d_e2p, d_wts, out2, T, cols], {"tokens": T})
+    torch.cuda.synchronize()
+    for name, got in (("finalize", from_dev(out)), ("finalize (manifest entry)", from_dev(out2))):
+        gn, wn = (got & 0x7FFF) > 0x7F80, (want & 0x7FFF) > 0x7F80
+        assert np.array_equal(gn, wn), f"{name}: NaN positions differ ({gn.sum()} vs {wn.sum()})"
+        print(f"  {name}: {gn.sum()} NaN, {((got & 0x7FFF) == 0x7F80).sum()} inf", flush=True)
+        assert np.array_equal(got[~gn], want[~wn]), f"{name}: non-NaN values differ"

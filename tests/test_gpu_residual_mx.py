@@ -301,3 +301,40 @@ def test_manifest_ops_through_module_launch(ctx):
     k3h.ManifestOp(ctx, "land_add_attnres_rms_bf16_v2_nb1", ops["land_add_attnres_rms_bf16_v2_nb1"])(args, env)
     torch.cuda.synchronize()
     assert not from_dev(p2).any() and not from_dev(nrm).any()
+
+
+@pytest.mark.parametrize("nb", [0, 1, 4])
+def test_k1b_special_values(ctx, nb):
+    """Specials (NaN of either sign, +-inf, +-max finite, the smallest subnormal,
+    -0) planted in partial, prefix and the block candidates of some rows: landing,
+    AttnRes scores (NaN / inf scores through the softmax's exp) and the norm
+    propagate them exactly as the oracle, through the 128-thread entry and the
+    typed nb entry (vector-split body)."""
+    specials = np.array([0x7FC0, 0xFFC1, 0x7F80, 0xFF80, 0x7F7F, 0xFF7F, 0x0001, 0x8000], np.uint16)
+    B = 16
+    _case(f"k1b special values nb={nb}")
+    prefix, partial, blocks, sw, gamma = _k1_inputs(400 + nb, B)
+    g = rng(401 + nb)
+    for a, n in ((partial, 12), (prefix, 12), (blocks, 24)):
+        flat = a.reshape(-1)
+        flat[g.choice(flat.size, n, replace=False)] = specials[np.arange(n) % specials.size]
+    want_p2, want_n = O.land_add_attnres_rms(partial, prefix, blocks, sw, gamma, nb, 0, B)
+
+    def check(name, got, want):
+        gn, wn = (got & 0x7FFF) > 0x7F80, (want & 0x7FFF) > 0x7F80
+        assert np.array_equal(gn, wn), f"{name}: NaN positions differ ({gn.sum()} vs {wn.sum()})"
+        assert np.array_equal(got[~gn], want[~wn]), f"{name}: non-NaN values differ"
+
+    entries = [("128-thread entry", ctx.land_add_attnres_rms)]
+    if nb > 0:
+        entries.append(("typed nb entry", ctx.land_add_attnres_rms_nb))
+    for label, fn in entries:
+        p2 = torch.empty((B, H), dtype=torch.bfloat16, device="cuda")
+        nrm = torch.empty_like(p2)
+        fn(to_dev(partial), to_dev(prefix), to_dev(blocks), to_dev(sw), to_dev(gamma), p2, nrm, nb, 0, B)
+        torch.cuda.synchronize()
+        got_n = from_dev(nrm)
+        print(f"  {label}: normed NaN rows {int(((got_n & 0x7FFF) > 0x7F80).any(axis=1).sum())} of {B}",
+              flush=True)
+        check(f"{label} prefix2", from_dev(p2), want_p2)
+        check(f"{label} normed", got_n, want_n)
