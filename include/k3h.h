@@ -60,7 +60,8 @@ K3H_API const char* k3h_error_string(int code);
 K3H_API int k3h_runtime_version(int* version);
 
 /* ---- context: code objects by module key ---------------------------------
- * <dir>/<module key>.hsaco, loaded on first use (e.g. "k3_residual_v2+LAND_BF16=1"). */
+ * <dir>/<module key>.hsaco, loaded on first use (e.g. "k3_residual_v2+LAND_BF16=1")
+ * into the device current at that moment: use one context per device. */
 K3H_API int k3h_ctx_create(const char* codeobj_dir, k3h_ctx_t* out);
 K3H_API int k3h_ctx_destroy(k3h_ctx_t ctx);
 K3H_API int k3h_ctx_function(k3h_ctx_t ctx, const char* module_key, const char* entry,
