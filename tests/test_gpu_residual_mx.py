@@ -315,9 +315,19 @@ def test_k1b_special_values(ctx, nb):
     _case(f"k1b special values nb={nb}")
     prefix, partial, blocks, sw, gamma = _k1_inputs(400 + nb, B)
     g = rng(401 + nb)
-    for a, n in ((partial, 12), (prefix, 12), (blocks, 24)):
-        flat = a.reshape(-1)
-        flat[g.choice(flat.size, n, replace=False)] = specials[np.arange(n) % specials.size]
+    # one special per row in rows 0..11 (rows 12..15 clean), in partial, prefix or a
+    # block candidate in turn, so that finite specials take their own paths (a
+    # largest-finite value overflows the sum of squares, a subnormal or -0 does not)
+    for r in range(12):
+        sv = specials[r % specials.size]
+        c = int(g.integers(0, H))
+        tgt = r % 3
+        if tgt == 0:
+            partial[r, c] = sv
+        elif tgt == 1:
+            prefix[r, c] = sv
+        else:
+            blocks[r, int(g.integers(0, max(nb, 1))), c] = sv
     want_p2, want_n = O.land_add_attnres_rms(partial, prefix, blocks, sw, gamma, nb, 0, B)
 
     def check(name, got, want):
