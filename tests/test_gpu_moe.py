@@ -83,9 +83,9 @@ def test_router_topk_ties(ctx, topk):
 @pytest.mark.parametrize("topk", [8, 16])
 def test_router_topk_near_ties(ctx, topk):
     """Rows whose largest logits lie a few ulps apart (and rows with an infinite
-    logit): the typed call ranks by the hardware logistic first, so
-    here its approximate order can differ from the exact one near the top-k
-    boundary; the exact keys must still decide the picks and their order."""
+    logit): the keys near the top-k boundary differ in their last bits, and the
+    exact keys must decide the picks and their order (a kernel that ranked by an
+    approximate logistic first would be caught here)."""
     _case(f"router_topk near ties topk={topk}")
     T = 95
     g = rng(1770 + topk)
@@ -103,6 +103,38 @@ def test_router_topk_near_ties(ctx, topk):
     idx, wts = _run_router(ctx, S, bias, rs, T, topk)
     _eq("idx", idx, want_i)
     _eq("wts", wts.view(np.uint32), want_w.view(np.uint32))
+
+
+@pytest.mark.parametrize("topk", [8, 16])
+def test_router_topk_candidate_edges(ctx, topk):
+    """Rows at the edges of the key order: 40 experts within a few ulps of each
+    other at the top of a row (in one lane-half and spread over slots), every
+    logistic 0 or 1 (keys equal to the biases, or the biases plus one),
+    infinite logits, -inf and +inf biases (infinite keys tie and go to the
+    smallest ids), and a second bias vector finite for five experts only, so
+    that the top-k reaches into the -inf keys."""
+    _case(f"router_topk candidate edges topk={topk}")
+    T = 12
+    g = rng(1990 + topk)
+    S = g.standard_normal((T, 224), dtype=np.float32)
+    close = (np.float32(3.0).view(np.int32) + g.integers(0, 3, 40)).astype(np.int32)
+    S[1, :40] = close.view(np.float32)
+    S[2, :] = S[1, :]
+    S[3, 100:140] = close.view(np.float32)
+    S[5, :] = np.float32(-200.0)  # every logistic 0: keys are the biases
+    S[6, ::7] = np.inf
+    S[7, :] = np.float32(40.0)  # every logistic 1
+    rs = to_bf16(np.array([2.5], np.float32))
+    b1 = (g.standard_normal(224) * 0.01).astype(np.float32)
+    b1[30:224:3] = -np.inf
+    b1[[3, 77, 150]] = np.inf
+    b2 = (g.standard_normal(224) * 0.01).astype(np.float32)
+    b2[5:] = -np.inf
+    for bias in (b1, b2):
+        want_i, want_w = O.router_topk(S, bias, rs[0], T, topk)
+        idx, wts = _run_router(ctx, S, bias, rs, T, topk)
+        _eq("idx", idx, want_i)
+        _eq("wts", wts.view(np.uint32), want_w.view(np.uint32))
 
 
 def test_argmax_f32(ctx):
