@@ -183,3 +183,22 @@ def test_wrappers_reject_undersized_buffers(monkeypatch):
         ctx.moe_permute_mx(u8(10 * 1024 - 1), u8(10 * 32), i32(8), i32(1), 1024, u8(8 * 1024),
                            u8(8 * 32), tokens=10)
     ctx.close()
+
+
+def test_missing_code_objects_fail_loudly(tmp_path):
+    """A context over a directory without the gfx950 code objects: the typed
+    calls and the entry lookup return K3H_ENOMODULE (and the Python mirror
+    raises); nothing falls back to another implementation."""
+    L = k3h.lib()
+    h = ctypes.c_void_p()
+    assert L.k3h_ctx_create(str(tmp_path).encode(), ctypes.byref(h)) == 0
+    try:
+        assert L.k3h_residual_rms_mxfp8(h, None, A, A, A, A, A, A, None, 1e-6, 1) == k3h.K3H_ENOMODULE
+        assert L.k3h_moe_quant(h, None, A, A, A, 1, 7168) == k3h.K3H_ENOMODULE
+        fn = ctypes.c_void_p()
+        assert L.k3h_ctx_function(h, b"k3h_fused", b"k3h_residual_rms_mxfp8",
+                                  ctypes.byref(fn)) == k3h.K3H_ENOMODULE
+    finally:
+        assert L.k3h_ctx_destroy(h) == 0
+    with pytest.raises(k3h.K3HError):
+        k3h.Ctx(str(tmp_path)).function("k3h_fused", "k3h_residual_rms_mxfp8")
