@@ -4,6 +4,7 @@ table.  No GPU: the CSVs and the ops JSON are written here."""
 import csv
 import json
 import os
+import subprocess
 import sys
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -142,3 +143,12 @@ def test_trace_table_takes_clean_flush_launches(tmp_path):
     assert cp[3] == "3.00" and cp[4] == f"{8_000_000 / 3e-6 / 1e9:.1f}"   # median of 2, 4, 3
     rt = [c.strip() for c in next(l for l in md if l.startswith("| EP routing tables")).strip("|").split("|")]
     assert rt[3] == "7.00"                                                # 1+2+4 (median of 6, 8, 7)
+
+
+def test_more_than_one_gpu_is_refused():
+    """bench.py measures one GPU: --gpus N > 1 exits with status 2 and says so,
+    before touching a device."""
+    r = subprocess.run([sys.executable, os.path.join(REPO, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU only" in r.stderr
