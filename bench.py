@@ -339,6 +339,7 @@ def _bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0, gr
     parts = torch.empty(2048, dtype=torch.float32, device="cuda")
     add("per-tensor fp8 pair (amax+apply)", "kern_quant_fp8_{amax,apply}_v2", f"{T}x{H}",
         2 * T * H * 2 + T * H, timed(lambda: ctx.quant_fp8_tensor(x, q, sc, parts, T * H, stream=s)),
+        note="amax pass keeps x in the MALL; the apply pass reads it from there",
         cpu=O and (lambda: O.quant_fp8_apply(xh, T * H, O.quant_fp8_amax(xh, T * H, 2048), 2048)))
     del xh
     del ro, q, sf
