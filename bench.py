@@ -436,6 +436,7 @@ def _bench_ops(ctx, reps: int, out_path: str | None, cpu_budget: float = 0.0, gr
     psf = torch.empty((tpad, H // 32), dtype=torch.uint8, device="cuda")
     add("MXFP8 permute (cfg 5c)", "k3h_moe_permute_mx", f"{tpad} rows x {H}", 2 * tpad * (H + H // 32),
         timed(lambda: ctx.moe_permute_mx(x8, sf8, rmap, tp, H, pq, psf, stream=s)),
+        note="a token's repeated rows read from the MALL",
         cpu=O and (lambda a=(h(x8), h(sf8), h(rmap)): O.moe_permute_mx(a[0], a[1], a[2], tpad, H)))
     del pq, psf, x8, sf8
     fc2 = syn("5/fc2", (tpad, H))
